@@ -1,0 +1,275 @@
+#!/usr/bin/env python3
+"""Benchmark of the int4/int8 quantized-inference path on one MI355X.
+
+Headline (BASELINE.json ``metric``): int4-g128 GEMV HBM GB/s at
+M=1 x K=4096 x N=11008 (fp16 activations / scales / output, fp32 accumulate).
+A step is one launch of the dequant-matvec over one batch (one activation
+row).  The same JSON line carries the prefill GEMM TFLOP/s and the other
+configurations under ``extra``.
+
+Method:
+  * inputs are uploaded once and resident in HBM before timing;
+  * each configuration cycles through R weight/scale replicas whose total
+    exceeds MI355X's 256 MB Infinity Cache, so weights stream from HBM;
+  * launches are captured in a HIP graph (torch.cuda.CUDAGraph over the
+    library's launches on the capture stream) and replayed, so host launch
+    cost does not gap the GPU; HIP events on that stream bracket the replays;
+  * roofline.achieved = algorithmic bytes (or FLOPs) per launch / average
+    launch duration over the timed replays.
+The CPU baseline is the oracle's restatement of the reference NumPy path
+(examples/38_quantized_matmul.py:215-232), timed on this host on the same
+inputs, median of timed runs after warm-up as in
+examples/38_quantized_matmul.py:300-340.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+LLC_BYTES = 256 << 20
+METRIC = "W4 GEMV HBM GB/s (% of peak) @1x4096x11008; W4 prefill GEMM TFLOP/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+class Case:
+    """One dequant-matmul / dequant configuration with device replicas."""
+
+    def __init__(self, kind, wbits, M, N, K, G, lo, hi, seed=0, min_bytes=LLC_BYTES * 5 // 4,
+                 max_replicas=64):
+        import torch
+        from locomp_amd import synth, _lib
+        self.kind, self.wbits, self.M, self.N, self.K, self.G = kind, wbits, M, N, K, G
+        if kind == "dequant":
+            W, S = synth.dequant_case(wbits, N, K, G, lo, hi, seed=seed)
+            X = None
+        else:
+            X, W, S = synth.matvec_case(wbits, M, N, K, G, lo, hi, seed=seed)
+        self.host = (X, W, S)
+        self.w_bytes = W.nbytes
+        self.s_bytes = S.nbytes
+        if kind == "dequant":
+            self.out_elems = N * K
+            self.algo_bytes = W.nbytes + S.nbytes + N * K * 2
+            self.flops = 0
+        else:
+            self.out_elems = M * N
+            self.algo_bytes = W.nbytes + S.nbytes + X.nbytes + M * N * 2
+            self.flops = 2 * M * N * K
+        per = W.nbytes + S.nbytes + (self.out_elems * 2 if kind == "dequant" else 0)
+        self.R = max(1, min(max_replicas, math.ceil(min_bytes / per)))
+        w0, s0 = _dev(W), _dev(S)
+        self.W = [w0] + [w0.clone() for _ in range(self.R - 1)]
+        self.S = [s0] + [s0.clone() for _ in range(self.R - 1)]
+        self.X = _dev(X) if X is not None else None
+        nout = self.R if kind == "dequant" else 1
+        self.O = [torch.empty(self.out_elems, dtype=torch.float16, device="cuda") for _ in range(nout)]
+        self.lib = _lib.load()
+        torch.cuda.synchronize()
+
+    def launch(self, i, stream):
+        r = i % self.R
+        lib, K, G, N, M = self.lib, self.K, self.G, self.N, self.M
+        vp = ctypes.c_void_p
+        if self.kind == "dequant":
+            fn = lib.locomp_amd_dequant_int4 if self.wbits == 4 else None
+            rc = fn(vp(self.W[r].data_ptr()), vp(self.S[r].data_ptr()), vp(self.O[r].data_ptr()),
+                    K, K // 2, K // G, G, N, 1, 1, stream)
+        elif self.wbits == 4:
+            rc = lib.locomp_amd_dequant_matvec_int4(
+                vp(self.X.data_ptr()), vp(self.W[r].data_ptr()), vp(self.S[r].data_ptr()),
+                vp(self.O[0].data_ptr()), K, K // 2, K // G, G, N, M, 1, 1, 1, stream)
+        else:
+            rc = lib.locomp_amd_dequant_matvec_int8(
+                vp(self.X.data_ptr()), vp(self.W[r].data_ptr()), vp(self.S[r].data_ptr()),
+                vp(self.O[0].data_ptr()), K, K // G, G, N, M, 1, 1, 1, stream)
+        if rc != 0:
+            raise RuntimeError(f"launch failed: {rc}")
+
+    def result(self):
+        return self.O[0].cpu().numpy()
+
+
+def time_graph(case, steps, warmup, per_graph=None):
+    """Capture `per_graph` launches in a graph; replay to cover warmup + steps.
+
+    Returns (seconds for `steps` launches, launches actually timed)."""
+    import torch
+    per_graph = per_graph or case.R * max(1, math.ceil(64 / case.R))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(min(per_graph, 2 * case.R)):   # eager warm-up (first-launch costs)
+            case.launch(i, ctypes.c_void_p(s.cuda_stream))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(per_graph):
+            case.launch(i, ctypes.c_void_p(s.cuda_stream))
+    torch.cuda.synchronize()
+    n_warm = max(1, math.ceil(warmup / per_graph))
+    n_timed = max(1, math.ceil(steps / per_graph))
+    with torch.cuda.stream(s):
+        for _ in range(n_warm):
+            g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(n_timed):
+            g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3, n_timed * per_graph
+
+
+def cpu_baseline(case, budget_s=20.0):
+    """Oracle (restated reference NumPy path) on the host, same inputs."""
+    from oracle import quant_ref as ref
+    X, W, S = case.host
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        blas_threads = int(os.environ.get("OPENBLAS_NUM_THREADS", os.environ.get("OMP_NUM_THREADS", "1")))
+
+    def run():
+        return ref.fast_numpy_matvec_int4(X[0].astype(np.float32), W, S.astype(np.float32), case.G)
+
+    t0 = time.perf_counter()
+    run()
+    one = time.perf_counter() - t0
+    runs = int(max(3, min(15, budget_s / max(one, 1e-3) - 2)))
+    for _ in range(2):
+        run()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    med = sorted(ts)[len(ts) // 2]
+    return {
+        "value": round(case.algo_bytes / med / 1e9, 3), "unit": "GB/s",
+        "cores": int(blas_threads),
+        "kind": "port",
+        "sample": (f"oracle fast_numpy_matvec_int4 (examples/38_quantized_matmul.py:215-232) on the "
+                   f"full M=1 x 4096 x 11008 g128 inputs, median of {runs} runs after 2 warm-ups, "
+                   f"{med * 1e3:.1f} ms/call; elementwise NumPy is single-threaded, the BLAS "
+                   f"product used {blas_threads} threads; host os.cpu_count()={os.cpu_count()}, "
+                   f"affinity={len(os.sched_getaffinity(0))}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of extra cases to run (default all)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("no HIP device visible", file=sys.stderr)
+        return 1
+    from locomp_amd import synth
+
+    c3 = synth.CFG3
+    log("case gemv_w4a16 M=1")
+    head = Case("matvec", 4, 1, c3["N"], c3["K"], c3["G"], c3["lo"], c3["hi"])
+    t, n = time_graph(head, args.steps, args.warmup)
+    us = t / n * 1e6
+    gbs = head.algo_bytes / (t / n) / 1e9
+
+    extra = {}
+    only = set(filter(None, args.only.split(","))) if args.only else None
+
+    def want(name):
+        return only is None or name in only
+
+    def run_case(name, case, bound):
+        steps = max(200, args.steps // 8)
+        tt, nn = time_graph(case, steps, max(50, args.warmup // 8))
+        per = tt / nn
+        d = {"us_per_launch": round(per * 1e6, 3), "GB_s": round(case.algo_bytes / per / 1e9, 1),
+             "replicas": case.R, "launches": nn}
+        if case.flops:
+            d["TFLOP_s"] = round(case.flops / per / 1e12, 2)
+        if bound == "hbm":
+            d["frac_hbm"] = round(case.algo_bytes / per / 1e9 / HBM_PEAK_GBS, 4)
+        else:
+            d["frac_mfma_f16"] = round(case.flops / per / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+        extra[name] = d
+        log(name, d)
+
+    if want("gemm_prefill"):
+        c = synth.CFG5A
+        run_case("gemm_prefill_w4a16_2048x4096x4096_g128",
+                 Case("matvec", 4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
+                      min_bytes=0, max_replicas=4), "mfma")
+    for M in (4, 16):
+        if want(f"gemv_m{M}"):
+            run_case(f"gemv_w4a16_M{M}", Case("matvec", 4, M, c3["N"], c3["K"], c3["G"], c3["lo"],
+                                                c3["hi"]), "hbm")
+    if want("dequant"):
+        c = synth.CFG2
+        run_case("dequant_int4_4096x4096_g32_f16",
+                 Case("dequant", 4, 0, c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm")
+    if want("w8a16"):
+        c = synth.CFG4
+        run_case("w8a16_M64_14336x4096",
+                 Case("matvec", 8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm")
+
+    cpu = None if args.no_cpu else cpu_baseline(head)
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded np.random.default_rng(0), draw order X, W, S)",
+        "config": {"workload": "gemv_w4a16 int4-g128 M=1 K=4096 N=11008, fp16 X/scales/Y, "
+                               "fp32 accumulate", "M": 1, "K": 4096, "N": 11008, "group": 128,
+                   "weight_replicas": head.R},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": head.algo_bytes,
+                     "avg_launch_us": round(us, 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

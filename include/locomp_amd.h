@@ -1,0 +1,129 @@
+/*
+ * locomp_amd C ABI: int4 / int8 weight-only dequantize and dequant-matmul on
+ * AMD Instinct MI355X (gfx950).
+ *
+ * This is the drop-in boundary for locomp's quantized-inference path.  In the
+ * reference (Zyora-Dev/locomp v1.0.0) every kernel launch reaches the GPU
+ * through a per-kernel generated shared object exporting
+ *     extern "C" void locomp_launch_<name>(int grid_x, int grid_y,
+ *                                          int block_x, int block_y,
+ *                                          void** args);
+ * (locomp/backends/rocm_codegen.py:304-340), bound with ctypes in
+ * locomp/api.py:949-990, with the kernel's integer constexprs baked into the
+ * generated source.  Each entry point below replaces one such generated
+ * launcher: it takes the same pointer arguments in the same order, then the
+ * same integer arguments in the same order (now run-time values), then the
+ * grid extent (rows N), then the extensions the reference lacks (activation
+ * rows M, element dtypes, a HIP stream).
+ *
+ * Conventions
+ *   - All pointers are device pointers; the library allocates nothing.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
+ *     is asynchronous: the caller synchronises.
+ *   - Return value: 0 on success; a negative LQ_ERR_* for invalid arguments
+ *     (nothing is launched); a positive hipError_t if the launch failed.
+ *   - Layouts (locomp examples/38_quantized_matmul.py:30-134,
+ *     examples/52_dequantize.py:27-74):
+ *       int4 W: uint8 [N, K/2], byte j of row n = (q[n,2j+1] << 4) | q[n,2j],
+ *               value (q - 8) * s
+ *       int8 W: int8  [N, K],   value q * s
+ *       scales: [N, K/G] row-major, s[n, k / G]  (G = K: per output channel)
+ *       X: [M, K] row-major;  O: [M, N] row-major;  O = X @ dequant(W)^T
+ *   - Dequantised values are float32(q - 8) * float32(s), rounded once to
+ *     the output dtype (bit-exact with the reference's NumPy path).
+ */
+#ifndef LOCOMP_AMD_H_
+#define LOCOMP_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LOCOMP_AMD_ABI_VERSION 1
+
+/* Element dtype codes. */
+enum {
+  LQ_F32 = 0,  /* locomp.Tensor (float32)           */
+  LQ_F16 = 1,  /* locomp.Float16                    */
+  LQ_BF16 = 2  /* locomp.BFloat16 (stored as 16 bits) */
+};
+
+/* Error codes (negative; positive values are hipError_t). */
+enum {
+  LQ_OK = 0,
+  LQ_ERR_SHAPE = -1,   /* inconsistent or unsupported sizes           */
+  LQ_ERR_DTYPE = -2,   /* unknown dtype code                          */
+  LQ_ERR_NULL = -3,    /* null pointer with a non-empty problem        */
+  LQ_ERR_POLICY = -4   /* unknown kernel policy                        */
+};
+
+/* Kernel policies (locomp_amd_set_policy). */
+enum {
+  LQ_POLICY_AUTO = 0,    /* fastest applicable kernel (default)          */
+  LQ_POLICY_GENERIC = 1  /* always the shape-generic kernels (for tests)  */
+};
+
+/* ABI version of the loaded library (== LOCOMP_AMD_ABI_VERSION). */
+int locomp_amd_abi_version(void);
+
+/* Static description of an error code (never NULL). */
+const char* locomp_amd_strerror(int code);
+
+/* Select the kernel policy for subsequent calls from this process.
+ * No counterpart in the reference (it has one generated kernel per shape);
+ * used by tests to run the shape-generic kernels on the same inputs. */
+int locomp_amd_set_policy(int policy);
+int locomp_amd_get_policy(void);
+
+/* Dequantize int4 -> OUT [N, K].
+ * Replaces locomp_launch_dequant_int4 generated for
+ * examples/52_dequantize.py:27-53 (args W, SCALES, OUT, K, HALF_K,
+ * NUM_SCALES, GROUP_SIZE; grid (N,), launched at examples/52_dequantize.py:90). */
+int locomp_amd_dequant_int4(const void* W, const void* SCALES, void* OUT,
+                            int64_t K, int64_t HALF_K, int64_t NUM_SCALES,
+                            int64_t GROUP_SIZE, int64_t N,
+                            int scale_dtype, int out_dtype, void* stream);
+
+/* Dequantize int8 -> OUT [N, K].
+ * Replaces locomp_launch_dequant_int8 generated for
+ * examples/52_dequantize.py:60-74 (args W, SCALES, OUT, K, NUM_SCALES,
+ * GROUP_SIZE; grid (N,), launched at examples/52_dequantize.py:104). */
+int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
+                            int64_t K, int64_t NUM_SCALES, int64_t GROUP_SIZE,
+                            int64_t N, int scale_dtype, int out_dtype,
+                            void* stream);
+
+/* O [M, N] = X [M, K] @ dequant_int4(W)^T, fp32 accumulation.
+ * Replaces locomp_launch_dequant_matvec_int4 generated for
+ * examples/38_quantized_matmul.py:30-87 (args X, W, scales, O, K_dim, HALF_K,
+ * NUM_SCALES, GROUP_SIZE; grid (N,), launched at
+ * examples/38_quantized_matmul.py:154).  M = 1 is the reference's matvec;
+ * M <= 64 runs the decode (skinny) kernel, larger M the prefill MFMA GEMM. */
+int locomp_amd_dequant_matvec_int4(const void* X, const void* W,
+                                   const void* scales, void* O,
+                                   int64_t K_dim, int64_t HALF_K,
+                                   int64_t NUM_SCALES, int64_t GROUP_SIZE,
+                                   int64_t N, int64_t M, int x_dtype,
+                                   int scale_dtype, int out_dtype,
+                                   void* stream);
+
+/* O [M, N] = X [M, K] @ dequant_int8(W)^T, fp32 accumulation.
+ * Replaces locomp_launch_dequant_matvec_int8 generated for
+ * examples/38_quantized_matmul.py:94-134 (args X, W, scales, O, K_dim,
+ * NUM_SCALES, GROUP_SIZE; grid (N,), launched at
+ * examples/38_quantized_matmul.py:170) and its copy quant_matvec_int8 in
+ * examples/58_benchmark_suite.py:241-264. */
+int locomp_amd_dequant_matvec_int8(const void* X, const void* W,
+                                   const void* scales, void* O,
+                                   int64_t K_dim, int64_t NUM_SCALES,
+                                   int64_t GROUP_SIZE, int64_t N, int64_t M,
+                                   int x_dtype, int scale_dtype,
+                                   int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOCOMP_AMD_H_ */

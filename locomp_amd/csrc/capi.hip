@@ -1,0 +1,152 @@
+// C ABI entry points: argument validation and kernel selection.
+// Declarations and conventions: include/locomp_amd.h.
+#include <atomic>
+
+#include "lq_common.h"
+
+namespace lq {
+int launch_dequant_int4(const void*, const void*, void*, int64_t, int64_t, int64_t, int, int, bool,
+                        hipStream_t);
+int launch_dequant_int8(const void*, const void*, void*, int64_t, int64_t, int64_t, int, int, bool,
+                        hipStream_t);
+template <int WBITS>
+int launch_skinny(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
+                  int, int, hipStream_t);
+template <int WBITS>
+int launch_generic(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
+                   int, int, int, hipStream_t);
+template <int WBITS>
+int launch_gemm(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
+                int, int, hipStream_t);
+int launch_zero_fill(void*, int64_t, int, hipStream_t);
+
+static std::atomic<int> g_policy{LQ_POLICY_AUTO};
+
+static inline bool dtype_ok(int d) { return d == LQ_F32 || d == LQ_F16 || d == LQ_BF16; }
+static inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Largest problem the 32-bit index arithmetic of the fast kernels accepts.
+constexpr int64_t kMax32 = (int64_t(1) << 31) - 1;
+
+// Checks shared by every entry point; returns LQ_OK or an error code.
+static int check_common(int64_t K, int64_t num_scales, int64_t G, int64_t N) {
+  if (K < 0 || N < 0 || num_scales < 0) return LQ_ERR_SHAPE;
+  if (G <= 0) return LQ_ERR_SHAPE;
+  if (num_scales * G != K) return LQ_ERR_SHAPE;
+  return LQ_OK;
+}
+
+static bool fast_allowed() { return g_policy.load(std::memory_order_relaxed) == LQ_POLICY_AUTO; }
+
+}  // namespace lq
+
+using namespace lq;
+
+// Kernel choice for the dequant-matmul entries (WBITS = 4 or 8).
+template <int WBITS>
+static int matmul_dispatch(const void* X, const void* W, const void* S, void* O, int64_t K,
+                           int64_t G, int64_t N, int64_t M, int xd, int sd, int od, hipStream_t st) {
+  if (!dtype_ok(xd) || !dtype_ok(sd) || !dtype_ok(od)) return LQ_ERR_DTYPE;
+  if (M < 0) return LQ_ERR_SHAPE;
+  if (M == 0 || N == 0) return LQ_OK;
+  if (!O) return LQ_ERR_NULL;
+  if (K == 0) return launch_zero_fill(O, M * N, od, st);
+  if (!X || !W || !S) return LQ_ERR_NULL;
+  const int64_t row_bytes = WBITS == 4 ? K / 2 : K;
+  const bool small_enough = M * K <= kMax32 && N * row_bytes <= kMax32 && M * N <= kMax32 &&
+                            N * (K / G) <= kMax32;
+  const bool fast = fast_allowed() && xd == LQ_F16 && small_enough && aligned(X, 16) &&
+                    aligned(W, 16) && K % 8 == 0;
+  if (fast) {
+    // Skinny (decode) kernel: 16-byte weight chunks per lane must lie in one
+    // group and in one row.
+    const int64_t lane_k = WBITS == 4 ? 32 : 16;
+    if (M <= 64 && K % lane_k == 0 && G % lane_k == 0)
+      return launch_skinny<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
+    // Prefill MFMA GEMM (int4): 32-k chunks per thread inside one group.
+    if constexpr (WBITS == 4) {
+      if (M > 64 && K % 64 == 0 && G % 32 == 0)
+        return launch_gemm<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
+    }
+  }
+  return launch_generic<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st);
+}
+
+extern "C" {
+
+int locomp_amd_abi_version(void) { return LOCOMP_AMD_ABI_VERSION; }
+
+const char* locomp_amd_strerror(int code) {
+  switch (code) {
+    case LQ_OK: return "success";
+    case LQ_ERR_SHAPE: return "inconsistent or unsupported sizes";
+    case LQ_ERR_DTYPE: return "unknown dtype code";
+    case LQ_ERR_NULL: return "null pointer for a non-empty problem";
+    case LQ_ERR_POLICY: return "unknown kernel policy";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "unknown error";
+}
+
+int locomp_amd_set_policy(int policy) {
+  if (policy != LQ_POLICY_AUTO && policy != LQ_POLICY_GENERIC) return LQ_ERR_POLICY;
+  g_policy.store(policy);
+  return LQ_OK;
+}
+
+int locomp_amd_get_policy(void) { return g_policy.load(); }
+
+int locomp_amd_dequant_int4(const void* W, const void* SCALES, void* OUT, int64_t K, int64_t HALF_K,
+                            int64_t NUM_SCALES, int64_t GROUP_SIZE, int64_t N, int scale_dtype,
+                            int out_dtype, void* stream) {
+  int rc = check_common(K, NUM_SCALES, GROUP_SIZE, N);
+  if (rc) return rc;
+  if (HALF_K * 2 != K) return LQ_ERR_SHAPE;
+  if (!dtype_ok(scale_dtype) || !dtype_ok(out_dtype)) return LQ_ERR_DTYPE;
+  if (N == 0 || K == 0) return LQ_OK;
+  if (!W || !SCALES || !OUT) return LQ_ERR_NULL;
+  const bool fast = fast_allowed() && HALF_K % 4 == 0 && GROUP_SIZE % 8 == 0 &&
+                    N * (HALF_K / 4) <= kMax32 && aligned(W, 4) && aligned(OUT, 16) &&
+                    N * NUM_SCALES <= kMax32;
+  return launch_dequant_int4(W, SCALES, OUT, N, K, GROUP_SIZE, scale_dtype, out_dtype, fast,
+                             static_cast<hipStream_t>(stream));
+}
+
+int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT, int64_t K,
+                            int64_t NUM_SCALES, int64_t GROUP_SIZE, int64_t N, int scale_dtype,
+                            int out_dtype, void* stream) {
+  int rc = check_common(K, NUM_SCALES, GROUP_SIZE, N);
+  if (rc) return rc;
+  if (!dtype_ok(scale_dtype) || !dtype_ok(out_dtype)) return LQ_ERR_DTYPE;
+  if (N == 0 || K == 0) return LQ_OK;
+  if (!W || !SCALES || !OUT) return LQ_ERR_NULL;
+  const bool fast = fast_allowed() && K % 8 == 0 && GROUP_SIZE % 8 == 0 &&
+                    N * (K / 8) <= kMax32 && aligned(W, 8) && aligned(OUT, 16) &&
+                    N * NUM_SCALES <= kMax32;
+  return launch_dequant_int8(W, SCALES, OUT, N, K, GROUP_SIZE, scale_dtype, out_dtype, fast,
+                             static_cast<hipStream_t>(stream));
+}
+
+int locomp_amd_dequant_matvec_int4(const void* X, const void* W, const void* scales, void* O,
+                                   int64_t K_dim, int64_t HALF_K, int64_t NUM_SCALES,
+                                   int64_t GROUP_SIZE, int64_t N, int64_t M, int x_dtype,
+                                   int scale_dtype, int out_dtype, void* stream) {
+  int rc = check_common(K_dim, NUM_SCALES, GROUP_SIZE, N);
+  if (rc) return rc;
+  if (HALF_K * 2 != K_dim) return LQ_ERR_SHAPE;
+  return matmul_dispatch<4>(X, W, scales, O, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
+                            out_dtype, static_cast<hipStream_t>(stream));
+}
+
+int locomp_amd_dequant_matvec_int8(const void* X, const void* W, const void* scales, void* O,
+                                   int64_t K_dim, int64_t NUM_SCALES, int64_t GROUP_SIZE,
+                                   int64_t N, int64_t M, int x_dtype, int scale_dtype,
+                                   int out_dtype, void* stream) {
+  int rc = check_common(K_dim, NUM_SCALES, GROUP_SIZE, N);
+  if (rc) return rc;
+  return matmul_dispatch<8>(X, W, scales, O, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
+                            out_dtype, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

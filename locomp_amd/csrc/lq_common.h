@@ -1,0 +1,113 @@
+// Shared device helpers for the gfx950 int4/int8 weight-only kernels.
+//
+// Weight formats (identical to locomp's examples 38 and 52):
+//   int4: uint8 [N, K/2]; byte j of row n holds k = 2j in the low nibble and
+//         k = 2j + 1 in the high nibble; w = (q - 8) * s[n, k / G].
+//   int8: int8 [N, K];  w = q * s[n, k / G].
+//   scales: [N, K/G] row-major (fp32 or fp16); G = K is per-output-channel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/locomp_amd.h"
+
+namespace lq {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- dtypes --
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(uint32_t(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// Materialises an fp32 value in a register.  The reference rounds the
+// dequantised product to fp32 and then to the output dtype; without this the
+// compiler may fold fmul + fptrunc into one mixed-precision FMA (a single
+// rounding straight to fp16), which is not bit-identical.
+__device__ __forceinline__ float round_f32(float v) {
+  __asm__ volatile("" : "+v"(v));
+  return v;
+}
+
+template <int DT> struct Elem;
+template <> struct Elem<LQ_F32>  { typedef float    T; };
+template <> struct Elem<LQ_F16>  { typedef half_t   T; };
+template <> struct Elem<LQ_BF16> { typedef uint16_t T; };
+
+template <int DT>
+__device__ __forceinline__ float load_f32(const void* p, size_t i) {
+  if constexpr (DT == LQ_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == LQ_F16) return float(static_cast<const half_t*>(p)[i]);
+  else return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void store_f32(void* p, size_t i, float v) {
+  if constexpr (DT == LQ_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (DT == LQ_F16) static_cast<half_t*>(p)[i] = half_t(v);
+  else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+// ------------------------------------------------------ bit-level unpack --
+
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+
+// One packed int4 dword (8 weights, k0..k7 in order) -> four half2 holding
+// (q - 8) for (k0,k1), (k2,k3), (k4,k5), (k6,k7), exactly.
+// Byte p is replicated into bytes 0 and 2 (v_perm_b32), masked to its low
+// nibble at bits 3:0 and its high nibble at bits 23:20, and OR-ed with
+// 0x6400 (1024.0h) in each half.  The low half is then 1024 + q_even and the
+// high half 1024 + 16 * q_odd, both exact in fp16.  One packed FMA
+// h * (1, 1/16) + (-1032, -72) maps both to q - 8 exactly (the products are
+// exact and the sum is representable, so the single rounding is exact).
+__device__ __forceinline__ half2_t int4_pair_to_h2(uint32_t w, int p) {
+  const half2_t mul = {half_t(1.0f), half_t(0.0625f)};
+  const half2_t add = {half_t(-1032.0f), half_t(-72.0f)};
+  const uint32_t sel = 0x00000000u | uint32_t(p) | (uint32_t(p) << 16);
+  const uint32_t u = __builtin_amdgcn_perm(w, w, sel);
+  const uint32_t t = (u & 0x00F0000Fu) | 0x64006400u;
+  return __builtin_elementwise_fma(as_h2(t), mul, add);
+}
+
+__device__ __forceinline__ void int4x8_to_h2(uint32_t w, half2_t out[4]) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) out[p] = int4_pair_to_h2(w, p);
+}
+
+// Two int8 weights (bytes 2p, 2p+1 of w) -> half2 exact: (b ^ 0x80) in the
+// low mantissa byte of 1024.0h gives 1024 + b + 128; subtract 1152.
+__device__ __forceinline__ void int8x4_to_h2(uint32_t w, half2_t out[2]) {
+  const half2_t off = {half_t(1152.0f), half_t(1152.0f)};
+  const uint32_t x = w ^ 0x80808080u;
+  // v_perm_b32 byte selectors: 0..3 pick from the 2nd operand (x), 4..7 from
+  // the 1st (0x64646464).  lo = bytes {b0', 0x64, b1', 0x64} (LSB first).
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
+  out[0] = as_h2(lo) - off;
+  out[1] = as_h2(hi) - off;
+}
+
+// ---------------------------------------------------------------- launch --
+
+__host__ __forceinline__ int check_launch() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? LQ_OK : int(e);
+}
+
+}  // namespace lq

@@ -1,0 +1,217 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars: dequantised weights bit-exact; dequant-matmul within rtol 1e-2 /
+atol 1e-2 for fp16 activations, rtol 1e-4 (+ atol 1e-5 * max|Y|) for fp32.
+"""
+
+import numpy as np
+import pytest
+
+from locomp_amd import synth
+from oracle import quant_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+lq = pytest.importorskip("locomp_amd")
+
+NP_OF = {"f32": np.float32, "f16": np.float16}
+
+
+def _dtype(name):
+    return lq.bfloat16 if name == "bf16" else NP_OF[name]
+
+
+def _up(a, dtype_name=None):
+    if dtype_name == "bf16":
+        return lq.tensor(a.astype(np.float32), dtype=lq.bfloat16)
+    return lq.tensor(np.ascontiguousarray(a))
+
+
+def _scales_f32(S, s_name):
+    return S.astype(np.float32)
+
+
+@pytest.fixture(params=["auto", "generic"])
+def policy(request):
+    lq.set_policy(0 if request.param == "auto" else 1)
+    yield request.param
+    lq.set_policy(0)
+
+
+# ---------------------------------------------------------------- dequant --
+
+def _run_dequant4(W, S, N, K, G, od):
+    Wg, Sg = _up(W), _up(S)
+    Og = lq.empty(N * K, _dtype(od))
+    lq.dequant_int4[(N,), (128,)](Wg, Sg, Og, K, K // 2, K // G, G)
+    return Og.numpy().reshape(N, K)
+
+
+def _run_dequant8(W, S, N, K, G, od):
+    Wg, Sg = _up(W), _up(S)
+    Og = lq.empty(N * K, _dtype(od))
+    lq.dequant_int8[(N,), (128,)](Wg, Sg, Og, K, K // G, G)
+    return Og.numpy().reshape(N, K)
+
+
+def _bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view({2: np.uint16, 4: np.uint32}[a.dtype.itemsize])
+
+
+@pytest.mark.parametrize("sd", ["f16", "f32"])
+@pytest.mark.parametrize("od", ["f16", "f32", "bf16"])
+@pytest.mark.parametrize("N,K,G", [(64, 256, 32), (37, 96, 8), (5, 64, 64), (3, 30, 6), (16, 4, 2)])
+def test_dequant_int4_bitexact(policy, sd, od, N, K, G):
+    W, S = synth.dequant_case(4, N, K, G, 0.001, 0.01, s_dtype=NP_OF[sd], seed=N + K)
+    got = _run_dequant4(W, S, N, K, G, od)
+    want = ref.cast_out(ref.dequant_int4_ref(W, S, N, K, G), od)
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("sd", ["f16", "f32"])
+@pytest.mark.parametrize("od", ["f16", "f32", "bf16"])
+@pytest.mark.parametrize("N,K,G", [(64, 256, 32), (37, 96, 8), (5, 64, 64), (3, 30, 6)])
+def test_dequant_int8_bitexact(policy, sd, od, N, K, G):
+    W, S = synth.dequant_case(8, N, K, G, 0.002, 0.02, s_dtype=NP_OF[sd], seed=N * K)
+    got = _run_dequant8(W, S, N, K, G, od)
+    want = ref.cast_out(ref.dequant_int8_ref(W, S, N, K, G), od)
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+def test_dequant_int4_cfg2_full_bitexact():
+    c = synth.CFG2
+    W, S = synth.dequant_case(4, c["N"], c["K"], c["G"], c["lo"], c["hi"])
+    got = _run_dequant4(W, S, c["N"], c["K"], c["G"], "f16")
+    want = ref.dequant_int4_ref(W, S, c["N"], c["K"], c["G"]).astype(np.float16)
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+def test_dequant_reference_selfcheck_shapes():
+    """examples/52_dequantize.py:146-170: seed 42, G=32, three shapes, fp32."""
+    rng = np.random.default_rng(42)
+    for N, K in [(64, 256), (128, 512), (256, 1024)]:
+        w = rng.standard_normal((N, K)).astype(np.float32) * 0.5
+        packed, scales = ref.quantize_int4_ref(w, 32)
+        got = lq.gpu_dequant_int4(packed, scales, N, K, 32)
+        want = ref.dequant_int4_ref(packed, scales, N, K, 32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        absmax = np.abs(w.reshape(N, K // 32, 32)).max(axis=2)
+        s8 = (absmax / 127.0).astype(np.float32)
+        q8 = np.clip(np.round(w / (np.repeat(s8, 32, axis=1) + 1e-10)), -128, 127).astype(np.int8)
+        got8 = lq.gpu_dequant_int8(q8, s8, N, K, 32)
+        want8 = q8.astype(np.float32) * np.repeat(s8, 32, axis=1)
+        assert np.array_equal(got8.view(np.uint32), want8.view(np.uint32))
+
+
+# --------------------------------------------------------------- matvec --
+
+def _matvec(wbits, X, W, S, N, K, G, od):
+    M = X.shape[0]
+    Xg, Wg, Sg = _up(X), _up(W), _up(S)
+    Og = lq.empty((M, N), _dtype(od))
+    if wbits == 4:
+        lq.dequant_matvec_int4[(N,), (128,)](Xg, Wg, Sg, Og, K, K // 2, K // G, G)
+    else:
+        lq.dequant_matvec_int8[(N,), (128,)](Xg, Wg, Sg, Og, K, K // G, G)
+    return Og.numpy()
+
+
+def _oracle(wbits, X, W, S, G):
+    if wbits == 4:
+        return ref.fast_numpy_matvec_int4(X, W, S, G)
+    return ref.fast_numpy_matvec_int8(X, W, S, G)
+
+
+def _close(got, want, fp32=False):
+    got = got.astype(np.float32)
+    if fp32:
+        atol = 1e-5 * max(1.0, float(np.abs(want).max()))
+        np.testing.assert_allclose(got, want, rtol=1e-4, atol=atol)
+    else:
+        np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("wbits", [4, 8])
+@pytest.mark.parametrize("M,N,K,G", [
+    (1, 64, 256, 32), (4, 100, 512, 128), (16, 48, 1024, 1024), (3, 17, 96, 32),
+    (1, 192, 576, 32), (1, 576, 1536, 32), (33, 40, 256, 64), (64, 80, 512, 512),
+    (2, 7, 40, 8), (5, 9, 16, 16)])
+def test_matvec_fp16_small(policy, wbits, M, N, K, G):
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=M * 1000 + N)
+    got = _matvec(wbits, X, W, S, N, K, G, "f16")
+    _close(got, _oracle(wbits, X, W, S, G))
+
+
+@pytest.mark.parametrize("M,N,K,G", [(96, 160, 256, 128), (130, 64, 512, 32), (256, 256, 1024, 64)])
+def test_matmul_prefill_small(policy, M, N, K, G):
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K)
+    got = _matvec(4, X, W, S, N, K, G, "f16")
+    _close(got, _oracle(4, X, W, S, G))
+
+
+def test_cfg1_w8a32_fp32():
+    c = synth.CFG1
+    X, W, S = synth.matvec_case(8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
+                                x_dtype=np.float32, s_dtype=np.float32)
+    got = _matvec(8, X, W, S, c["N"], c["K"], c["G"], "f32")
+    _close(got, _oracle(8, X, W, S, c["G"]), fp32=True)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_cfg3_gemv_w4a16_full(M):
+    c = synth.CFG3
+    X, W, S = synth.matvec_case(4, M, c["N"], c["K"], c["G"], c["lo"], c["hi"])
+    got = _matvec(4, X, W, S, c["N"], c["K"], c["G"], "f16")
+    _close(got, _oracle(4, X, W, S, c["G"]))
+
+
+def test_cfg4_w8a16_m64_full():
+    c = synth.CFG4
+    X, W, S = synth.matvec_case(8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"])
+    got = _matvec(8, X, W, S, c["N"], c["K"], c["G"], "f16")
+    _close(got, _oracle(8, X, W, S, c["G"]))
+
+
+def test_cfg5a_prefill_full():
+    c = synth.CFG5A
+    X, W, S = synth.matvec_case(4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"])
+    got = _matvec(4, X, W, S, c["N"], c["K"], c["G"], "f16")
+    # Oracle on a row subset (the full fp32 product is 69 GFLOP on the host).
+    rows = np.r_[0:64, 1000:1064, c["M"] - 64:c["M"]]
+    _close(got[rows], _oracle(4, X[rows], W, S, c["G"]))
+    assert np.isfinite(got.astype(np.float32)).all()
+
+
+def test_reference_fp32_matvec_api():
+    """examples/38_quantized_matmul.py:312-321 flow: quantize_int4, then gpu_matvec_int4."""
+    rng = np.random.default_rng(42)
+    for N, K in [(256, 256), (512, 512)]:
+        w = rng.standard_normal((N, K)).astype(np.float32) * 0.1
+        x = rng.standard_normal(K).astype(np.float32) * 0.1
+        wp, s = ref.quantize_int4(w, 32)
+        got = lq.gpu_matvec_int4(x, wp, s, 32)
+        _close(got, ref.fast_numpy_matvec_int4(x, wp, s, 32), fp32=True)
+        w8, s8 = ref.quantize_int8(w, 32)
+        got8 = lq.gpu_matvec_int8(x, w8, s8, 32)
+        _close(got8, ref.fast_numpy_matvec_int8(x, w8, s8, 32), fp32=True)
+
+
+def test_empty_and_zero_k():
+    Og = lq.zeros((2, 3), np.float16)
+    Og.torch.fill_(7)
+    lq.dequant_matvec_int4[(3,), (128,)](lq.empty(0, np.float16), lq.empty(0, np.uint8),
+                                         lq.empty(0, np.float16), Og, 0, 0, 0, 32)
+    assert (Og.numpy() == 0).all()
+    # N = 0: nothing launched, no error
+    lq.dequant_int4[(0,), (128,)](lq.empty(0, np.uint8), lq.empty(0, np.float16),
+                                  lq.empty(0, np.float16), 64, 32, 2, 32)
+
+
+def test_all_q8_gives_zero():
+    N, K, G = 48, 512, 128
+    W = np.full((N, K // 2), 0x88, np.uint8)
+    S = np.full((N, K // G), 0.01, np.float16)
+    X = np.random.default_rng(1).standard_normal((4, K)).astype(np.float16)
+    got = _matvec(4, X, W, S, N, K, G, "f16")
+    assert (got == 0).all()
