@@ -1,0 +1,1105 @@
+#pragma once
+// Decode-shaped dequant-matmul (M <= 64) for gfx950, and the shape-generic
+// fallback used for every case the fast kernels do not cover.
+//
+// Reference semantics: locomp examples/38_quantized_matmul.py:30-87 (int4)
+// and :94-134 (int8): O[m, n] = sum_k X[m, k] * w[n, k], fp32 accumulation.
+//
+// Fast kernel ("skinny"): fp16 activations, CDNA4 v_mfma_f32_16x16x32_f16.
+//   * A workgroup of 4 waves owns 16 weight rows and all M; the 4 waves split
+//     K (wave w takes k-steps w, w+4, ...) and their partial 16x(16*MT)
+//     tiles are summed through LDS at the end.
+//   * Lane l = (n = l % 16, quarter = l / 16) loads 16 packed bytes of row n
+//     per k-step with one 128-bit load; a wave instruction therefore covers
+//     16 rows x 64 contiguous bytes, and the 4 waves together stream 256
+//     contiguous bytes of every row.  Weights are touched exactly once.
+//   * The 16 bytes are dequantised in registers to exact fp16 (q - 8) (int4)
+//     or q (int8) and fed to the MFMA B operand as-is; the MFMA's K order is
+//     the same for A and B, so lane l's A operand is X[m = l % 16, same k].
+//   * Scales: when every k-step lies in one group (G % step == 0) the step's
+//     MFMA result is multiplied by s[n, g] in fp32 ("post-scale"); otherwise
+//     B is multiplied by its lane's scale in fp16 before the MFMA.
+#include "lq_common.h"
+
+namespace lq {
+
+constexpr int kSkThreads = 256;
+constexpr int kSkWaves = 4;
+constexpr int kSkBatch = 4;  // k-steps whose weight loads are issued together
+
+template <int WBITS> struct SkinnyGeom;
+template <> struct SkinnyGeom<4> { static constexpr int kLane = 32; static constexpr int kStep = 128; };
+template <> struct SkinnyGeom<8> { static constexpr int kLane = 16; static constexpr int kStep = 64; };
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ h8 make_h8(half2_t a, half2_t b, half2_t c, half2_t d) {
+  h8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+  return r;
+}
+
+// Row of a 16-byte X chunk: c / kc via an fp32 reciprocal (exact for the
+// chunk counts used here: c < 2^20, kc <= 2^14).
+__device__ __forceinline__ int chunk_row(int c, int kc, float inv_kc) {
+  int m = int((float(c) + 0.5f) * inv_kc);
+  return m;
+}
+
+template <int WBITS, int MT, bool POST, int SD, int OD>
+__global__ __launch_bounds__(kSkThreads) void skinny_mfma_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  typedef SkinnyGeom<WBITS> Geo;
+  constexpr int kMfmaPerLoad = Geo::kLane / 8;
+  __shared__ float4_t red[kSkWaves][MT][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nl = lane & 15;
+  const int quarter = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int n = n0 + nl;
+  const bool row_ok = n < N;
+  const int row_bytes = (WBITS == 4) ? (K >> 1) : K;
+  const uint8_t* wrow = W + size_t(row_ok ? n : 0) * row_bytes;
+  const int nsteps = (K + Geo::kStep - 1) / Geo::kStep;
+
+  float4_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int s0 = wave; s0 < nsteps; s0 += kSkWaves * kSkBatch) {
+    u32x4_t wv[kSkBatch];
+#pragma unroll
+    for (int b = 0; b < kSkBatch; ++b) {
+      const int s = s0 + b * kSkWaves;
+      const int k = s * Geo::kStep + quarter * Geo::kLane;
+      if (row_ok && s < nsteps && k < K) {
+        wv[b] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(wrow + (size_t(k) * WBITS >> 3)));
+      } else {
+        wv[b] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kSkBatch; ++b) {
+      const int s = s0 + b * kSkWaves;
+      if (s >= nsteps) break;
+      const int kl = s * Geo::kStep + quarter * Geo::kLane;  // lane's first k
+      const bool k_ok = kl < K;
+      float sc = 0.f;
+      half2_t sc2 = {half_t(0.f), half_t(0.f)};
+      if (POST) {
+        const int g = (s * Geo::kStep) / group;
+        sc = row_ok ? load_f32<SD>(S, size_t(n) * num_scales + g) : 0.f;
+      } else {
+        const int g = (k_ok ? kl : 0) / group;
+        const half_t h = row_ok ? half_t(load_f32<SD>(S, size_t(n) * num_scales + g)) : half_t(0.f);
+        sc2 = half2_t{h, h};
+      }
+      float4_t part[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) part[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < kMfmaPerLoad; ++i) {
+        half2_t hb[4];
+        if constexpr (WBITS == 4) {
+          const uint32_t word = wv[b][i];
+          int4x8_to_h2(word, hb);
+        } else {
+          int8x4_to_h2(wv[b][2 * i], hb);
+          int8x4_to_h2(wv[b][2 * i + 1], hb + 2);
+        }
+        if (!POST) {
+#pragma unroll
+          for (int p = 0; p < 4; ++p) hb[p] = hb[p] * sc2;
+        }
+        const h8 bop = make_h8(hb[0], hb[1], hb[2], hb[3]);
+        const int ka = kl + i * 8;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const int m = t * 16 + nl;
+          h8 aop = {};
+          if (m < M && k_ok) aop = *reinterpret_cast<const h8*>(X + size_t(m) * K + ka);
+          if (POST)
+            part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, part[t], 0, 0, 0);
+          else
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[t], 0, 0, 0);
+        }
+      }
+      if (POST) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[t] += part[t] * sc;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      float4_t v = red[0][t][lane] + red[1][t][lane] + red[2][t][lane] + red[3][t][lane];
+      // D layout of v_mfma_f32_16x16x32: lane holds rows 4*(lane/16)+r, column lane%16.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = t * 16 + quarter * 4 + r;
+        if (m < M && row_ok) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+      }
+    }
+  }
+}
+
+// -------------------------------------------- decode GEMV, LDS-staged --
+// M <= 16.  Latency-oriented design:
+//   * A workgroup of WAVES waves owns 16 * WAVES / KSPLIT weight rows; the
+//     KSPLIT waves of a 16-row tile take interleaved k-steps (wave ks takes
+//     steps ks, ks + KSPLIT, ...) and reduce through LDS at the end.  Many
+//     short waves (a few k-steps each) keep several waves per SIMD resident,
+//     which hides the MFMA and LDS latencies of each wave's chain.
+//   * Each wave issues *all* of its 128-bit weight loads (at most MAXJ per
+//     lane) before consuming any, so the whole weight matrix is in flight.
+//   * Activations and the workgroup's scale rows (contiguous in memory) are
+//     copied to LDS as raw 16-byte chunks whose global loads are issued
+//     before the weight loads: the vmcnt counter retires loads in order, so
+//     anything issued after the weights would wait for all of them.
+//   * Every load is unconditional (out-of-range lanes re-read a valid
+//     address) so the compiler counts outstanding loads down instead of
+//     draining them; the surplus values are neutralised (zero A operand, or
+//     an output column that is never written).
+//   * Per k-step: the LDS reads of the A operands come first, then the
+//     dequantisation, then two independent MFMA chains; with post-scaling
+//     the step's scale multiply is deferred by one step so it does not wait
+//     on the MFMA just issued.
+constexpr int kGvXPre = 2;        // 16-byte X chunks per lane prefetched before W
+constexpr int kGvSPre = 1;        // 16-byte scale chunks per lane prefetched before W
+
+template <int WBITS, bool POST, int SD, int OD, int WAVES, int KSPLIT, int MAXJ>
+__global__ __launch_bounds__(64 * WAVES) void gemv_lds_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  typedef SkinnyGeom<WBITS> Geo;
+  typedef typename Elem<SD>::T stype;
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int kMfmaPerLoad = Geo::kLane / 8;
+  constexpr int kRows = 16 * WAVES / KSPLIT;
+  constexpr int kSPerChunk = 16 / sizeof(stype);
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nl = lane & 15;
+  const int quarter = lane >> 4;
+  const int tile = wave / KSPLIT;
+  const int ks = wave % KSPLIT;
+  const int n0 = blockIdx.x * kRows;
+  const int n = n0 + tile * 16 + nl;
+  const bool row_ok = n < N;
+  const int xs = K + 8;                       // LDS row stride (halves), breaks bank aliasing
+  half_t* xl = reinterpret_cast<half_t*>(lds_raw);
+  stype* sl = reinterpret_cast<stype*>(lds_raw + size_t(M) * xs * 2);
+  const int rows_here = min(kRows, N - n0);
+  const int nsc = rows_here * num_scales;                // scale elements of this workgroup
+  const int schunks = (nsc + kSPerChunk - 1) / kSPerChunk;
+  float4_t* red = reinterpret_cast<float4_t*>(
+      lds_raw + size_t(M) * xs * 2 + ((size_t(kRows) * num_scales * sizeof(stype) + 15) & ~size_t(15)));
+  float* corr = reinterpret_cast<float*>(red + WAVES * 64);   // [nsteps][16]: BIAS * sum_k x[m, k]
+
+  // 1. activation / scale loads first (raw 16-byte chunks, clamped indices)
+  const int kc = K >> 3;                      // 16-byte chunks per X row
+  const int xchunks = M * kc;
+  const float inv_kc = 1.0f / float(kc);
+  u32x4_t xr[kGvXPre];
+#pragma unroll
+  for (int i = 0; i < kGvXPre; ++i) {
+    const int c = min(tid + i * kThreads, xchunks - 1);
+    xr[i] = *reinterpret_cast<const u32x4_t*>(X + size_t(c) * 8);
+  }
+  const stype* sg = static_cast<const stype*>(S) + size_t(n0) * num_scales;
+  u32x4_t sr[kGvSPre];
+#pragma unroll
+  for (int i = 0; i < kGvSPre; ++i) {
+    const int c = min(tid + i * kThreads, schunks - 1);
+    sr[i] = *reinterpret_cast<const u32x4_t*>(sg + size_t(c) * kSPerChunk);
+  }
+  // Keep the scheduler from interleaving the phases (it would otherwise hoist
+  // the LDS stores above the weight loads and wait for the X loads there).
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. all weight loads of this wave
+  const int row_bytes = (WBITS == 4) ? (K >> 1) : K;
+  const uint8_t* wrow = W + size_t(row_ok ? n : n0) * row_bytes;
+  const int nsteps = (K + Geo::kStep - 1) / Geo::kStep;
+  const int kmax = K - Geo::kLane;           // last valid lane start
+  u32x4_t wv[MAXJ];
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int s = ks + j * KSPLIT;
+    const int k = min(s * Geo::kStep + quarter * Geo::kLane, kmax);
+    wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + (size_t(k) * WBITS >> 3)));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. stage X and scales in LDS.  Unconditional stores at the clamped chunk
+  // index: lanes past the end rewrite the last chunk with the identical value.
+#pragma unroll
+  for (int i = 0; i < kGvXPre; ++i) {
+    const int c = min(tid + i * kThreads, xchunks - 1);
+    const int m = chunk_row(c, kc, inv_kc);
+    *reinterpret_cast<u32x4_t*>(xl + m * xs + (c - m * kc) * 8) = xperm8(xr[i]);
+  }
+  for (int c = tid + kGvXPre * kThreads; c < xchunks; c += kThreads) {
+    const int m = chunk_row(c, kc, inv_kc);
+    *reinterpret_cast<u32x4_t*>(xl + m * xs + (c - m * kc) * 8) =
+        xperm8(*reinterpret_cast<const u32x4_t*>(X + size_t(c) * 8));
+  }
+#pragma unroll
+  for (int i = 0; i < kGvSPre; ++i) {
+    const int c = min(tid + i * kThreads, schunks - 1);
+    *reinterpret_cast<u32x4_t*>(sl + c * kSPerChunk) = sr[i];
+  }
+  for (int c = tid + kGvSPre * kThreads; c < schunks; c += kThreads)
+    *reinterpret_cast<u32x4_t*>(sl + c * kSPerChunk) =
+        *reinterpret_cast<const u32x4_t*>(sg + size_t(c) * kSPerChunk);
+  __syncthreads();
+
+  const int nsteps_all = nsteps;
+  if constexpr (POST) {
+    // BIAS * sum of each activation row over each k-step (runs while the
+    // weight loads are still in flight).
+    const half2_t ones = {half_t(1.f), half_t(1.f)};
+    for (int t = tid; t < nsteps_all * 16; t += kThreads) {
+      const int st = t >> 4, m = t & 15;
+      float sum = 0.f;
+      if (m < M) {
+        const int k0 = st * Geo::kStep;
+        const int k1 = min(k0 + Geo::kStep, K);
+        for (int k = k0; k < k1; k += 8) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xl + m * xs + k);
+          sum = __builtin_amdgcn_fdot2(as_h2(v.x), ones, sum, false);
+          sum = __builtin_amdgcn_fdot2(as_h2(v.y), ones, sum, false);
+          sum = __builtin_amdgcn_fdot2(as_h2(v.z), ones, sum, false);
+          sum = __builtin_amdgcn_fdot2(as_h2(v.w), ones, sum, false);
+        }
+      }
+      corr[t] = sum * (WBITS == 4 ? kInt4Bias : kInt8Bias);
+    }
+    __syncthreads();
+  }
+
+  // 4. consume the weights in load order
+  const bool a_ok = nl < M;
+  const half_t* xrow = xl + nl * xs;
+  const int srow_i = (row_ok ? tile * 16 + nl : 0) * num_scales;
+  const half_t bias = half_t(WBITS == 4 ? kInt4Bias : kInt8Bias);
+  const half2_t bias2 = {bias, bias};
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  float4_t pend = {0.f, 0.f, 0.f, 0.f};   // previous step's unscaled partial (POST)
+  float pend_s = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int s = ks + j * KSPLIT;
+    if (s >= nsteps) break;
+    const int kl = s * Geo::kStep + quarter * Geo::kLane;
+    const bool k_ok = kl < K;
+    h8 aop[kMfmaPerLoad];
+#pragma unroll
+    for (int i = 0; i < kMfmaPerLoad; ++i) {
+      aop[i] = h8{};
+      if (a_ok && k_ok) aop[i] = *reinterpret_cast<const h8*>(xrow + kl + i * 8);
+    }
+    h8 bop[kMfmaPerLoad];
+#pragma unroll
+    for (int i = 0; i < kMfmaPerLoad; ++i) {
+      u32x4_t bw;
+      if constexpr (WBITS == 4) bw = int4x8_biased_kperm(wv[j][i]);
+      else bw = int8x8_biased_kperm(wv[j][2 * i], wv[j][2 * i + 1]);
+      if constexpr (!POST) {
+        const half_t h = half_t(load_f32<SD>(sl, srow_i + (k_ok ? kl : 0) / group));
+        const half2_t sc2 = {h, h};
+        bw.x = as_u32((as_h2(bw.x) - bias2) * sc2);
+        bw.y = as_u32((as_h2(bw.y) - bias2) * sc2);
+        bw.z = as_u32((as_h2(bw.z) - bias2) * sc2);
+        bw.w = as_u32((as_h2(bw.w) - bias2) * sc2);
+      }
+      bop[i] = __builtin_bit_cast(h8, bw);
+    }
+    if constexpr (POST) {
+      float4_t p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < kMfmaPerLoad; i += 2) {
+        p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[i], bop[i], p0, 0, 0, 0);
+        p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[i + 1], bop[i + 1], p1, 0, 0, 0);
+      }
+      acc += pend * pend_s;
+      pend = p0 + p1 - *reinterpret_cast<const float4_t*>(corr + s * 16 + quarter * 4);
+      pend_s = load_f32<SD>(sl, srow_i + (s * Geo::kStep) / group);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMfmaPerLoad; ++i)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[i], bop[i], acc, 0, 0, 0);
+    }
+  }
+  if constexpr (POST) acc += pend * pend_s;
+
+  // 5. reduce the KSPLIT partial tiles, write O
+  if constexpr (KSPLIT > 1) {
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int k2 = 1; k2 < KSPLIT; ++k2) acc += red[(wave + k2) * 64 + lane];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = quarter * 4 + r;
+    if (m < M && row_ok) store_f32<OD>(O, size_t(m) * N + n, acc[r]);
+  }
+}
+
+
+// ------------------------------------------ decode GEMV, row-contiguous --
+// int4, M <= 2.  Each wave owns RW whole weight rows; lane l covers the 32 k
+// starting at c * 2048 + 32 * l of every row (segment c < NSEG), so each wave
+// load instruction reads 1 KB contiguous of one row.  The lane's activations
+// for its k-range are loaded once (k-permuted to match the decoder) and reused
+// for all RW rows; their sum is kept to remove the decoder's +1032 bias.  Per
+// 16 bytes of weights: 7 VALU ops decode 4 x 8 weights to biased fp16 pairs,
+// 16 v_dot2_f32_f16 accumulate in fp32, and the 32-k partial is un-biased and
+// scaled (the 32 k lie in one group).  Rows are reduced across the wave with a
+// transposed butterfly (log2(RW) exchange stages, then 6 - log2(RW) plain
+// stages).  Load order: activations, scales, then all weights, so the
+// in-order vmcnt lets each row start as soon as its own bytes arrive.
+template <int M_, int NSEG, int RW, int SD, int OD>
+__global__ __launch_bounds__(256, 3) void gemv_rows_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  typedef typename Elem<SD>::T stype;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * RW;
+  const int half_k = K >> 1;
+
+  // 1. activations (k-permuted) for this lane's k-ranges
+  u32x4_t xv[M_][NSEG][4];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + lane * 32, K - 32);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xv[m][c][e] = *reinterpret_cast<const u32x4_t*>(X + size_t(m < M ? m : 0) * K + k0 + e * 8);
+    }
+  // 2. scales of (row, segment)
+  const stype* sp = static_cast<const stype*>(S);
+  stype sv[RW][NSEG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + lane * 32, K - 32);
+      const int n = min(n0 + r, N - 1);
+      sv[r][c] = sp[size_t(n) * num_scales + k0 / group];
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. all weights of this wave
+  u32x4_t wv[RW][NSEG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + lane * 32, K - 32);
+      const int n = min(n0 + r, N - 1);
+      wv[r][c] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(W + size_t(n) * half_k + (k0 >> 1)));
+    }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. permute activations, bias correction per (m, segment)
+  const half2_t ones = {half_t(1.f), half_t(1.f)};
+  float corr[M_][NSEG];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xv[m][c][e] = xperm8(xv[m][c][e]);
+        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].x), ones, sum, false);
+        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].y), ones, sum, false);
+        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].z), ones, sum, false);
+        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].w), ones, sum, false);
+      }
+      const bool valid = (m < M) && (c * 2048 + lane * 32 < K);
+      corr[m][c] = valid ? sum * kInt4Bias : 0.f;
+    }
+
+  // 5. rows
+  float acc[M_][RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int m = 0; m < M_; ++m) acc[m][r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const bool valid = c * 2048 + lane * 32 < K;
+      // four independent dot2 chains (one per dword) keep the VALU pipeline
+      // busy instead of waiting on one 16-long accumulate chain
+      float pe[M_][4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const u32x4_t b = int4x8_biased_kperm(wv[r][c][e]);
+#pragma unroll
+        for (int m = 0; m < M_; ++m) {
+          float t = __builtin_amdgcn_fdot2(as_h2(b.x), as_h2(xv[m][c][e].x), 0.f, false);
+          t = __builtin_amdgcn_fdot2(as_h2(b.y), as_h2(xv[m][c][e].y), t, false);
+          t = __builtin_amdgcn_fdot2(as_h2(b.z), as_h2(xv[m][c][e].z), t, false);
+          pe[m][e] = __builtin_amdgcn_fdot2(as_h2(b.w), as_h2(xv[m][c][e].w), t, false);
+        }
+      }
+      float part[M_];
+#pragma unroll
+      for (int m = 0; m < M_; ++m) part[m] = (pe[m][0] + pe[m][1]) + (pe[m][2] + pe[m][3]);
+      float sc;
+      if constexpr (SD == LQ_F32) sc = sv[r][c];
+      else if constexpr (SD == LQ_F16) sc = float(sv[r][c]);
+      else sc = bf16_to_f32(sv[r][c]);
+      sc = valid ? sc : 0.f;
+#pragma unroll
+      for (int m = 0; m < M_; ++m) acc[m][r] += (part[m] - corr[m][c]) * sc;
+      // consume in load order: no hoisting of later rows' decode (register
+      // pressure) and no early waits on their loads
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // 6. reduce each row over the 64 lanes: transposed butterfly
+#pragma unroll
+  for (int m = 0; m < M_; ++m) {
+    float v[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) v[r] = acc[m][r];
+    int cnt = RW;
+    int width = 32;
+#pragma unroll
+    for (; cnt > 1; cnt >>= 1, width >>= 1) {
+      const bool upper = (lane & width) != 0;
+      const int h = cnt >> 1;
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float keep = upper ? v[i + h] : v[i];
+        const float send = upper ? v[i] : v[i + h];
+        v[i] = keep + __shfl_xor(send, width, 64);
+      }
+    }
+#pragma unroll
+    for (; width > 0; width >>= 1) v[0] += __shfl_xor(v[0], width, 64);
+    // lane bits 5..(6 - log2 RW) name the row
+    int row = 0;
+    {
+      int w2 = 32;
+#pragma unroll
+      for (int c2 = RW; c2 > 1; c2 >>= 1, w2 >>= 1) row = row * 2 + ((lane & w2) ? 1 : 0);
+    }
+    const int lowmask = (64 / RW) - 1;
+    if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+  }
+}
+
+
+// ------------------------------------ decode GEMV, MFMA diagonal (M <= 4) --
+// int4, G % 128 == 0.  Each wave owns RW whole weight rows.  Lane l = (j, q)
+// (j = l % 16, q = l / 16) takes the 32 k at position p = 4j + q of every
+// 2048-k segment c, so one wave load instruction still reads 1 KB contiguous
+// of one row (lanes permuted).  The lane keeps its own activations for those
+// k in registers, shared by all rows.
+//
+// Decode, 5 VALU ops per 8 weights: t0 = (w & 0x000F000F) | 0x6400.. gives
+// (k0, k4) as 1024 + q; t1 = (w & 0x00F000F0) | .. gives (k1, k5) as
+// 1024 + 16q; t2, t3 the same on w >> 8 for (k2, k6), (k3, k7).  The matching
+// activations are k-permuted the same way and those multiplying a 16q half are
+// pre-divided by 16 (exact), so x' . v = x (q - 8) + x * BIAS with BIAS = 1032
+// or 72; the lane's BIAS * x sums are subtracted after the MFMA.
+//
+// Dot products run on the matrix core: MFMA t (t = 0..3, one per dword of the
+// lane's 16 bytes) computes D = A B with A[i][8q + e] = lane (i, q)'s
+// activations and B[8q + e][j] = lane (j, q)'s weights, so the diagonal
+// D[i][i] sums lanes (i, 0..3) = the 128 k of group i of the segment; the
+// other entries are discarded.  The diagonal element of group i sits in lane
+// i + 16 * (i / 4), accumulator register i % 4, where it is un-biased and
+// multiplied by the group scale; rows are then reduced across lanes.
+template <int M_, int NSEG, int RW, int SD, int OD>
+__global__ __launch_bounds__(256, 2) void gemv_diag_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  typedef typename Elem<SD>::T stype;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * RW;
+  const int half_k = K >> 1;
+  const int j = lane & 15, q = lane >> 4;
+  const int pos = 4 * j + q;
+  const bool diag = q == (j >> 2);
+  const int dreg = j & 3;
+
+  // 1. activations for this lane's k-ranges
+  u32x4_t xv[M_][NSEG][4];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + pos * 32, K - 32);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xv[m][c][e] = *reinterpret_cast<const u32x4_t*>(X + size_t(m < M ? m : 0) * K + k0 + e * 8);
+    }
+  // 2. scales of (row, segment): one group per lane quad
+  const stype* sp = static_cast<const stype*>(S);
+  stype sv[RW][NSEG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + pos * 32, K - 32);
+      const int n = min(n0 + r, N - 1);
+      sv[r][c] = sp[size_t(n) * num_scales + k0 / group];
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. all weights of this wave
+  u32x4_t wv[RW][NSEG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + pos * 32, K - 32);
+      const int n = min(n0 + r, N - 1);
+      wv[r][c] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(W + size_t(n) * half_k + (k0 >> 1)));
+    }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. activation operands: k-permute, /16 on the 16q pairs, bias sums
+  const half2_t sixteenth = {half_t(0.0625f), half_t(0.0625f)};
+  const half2_t ones = {half_t(1.f), half_t(1.f)};
+  float corr[M_][NSEG];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const bool valid = (m < M) && (c * 2048 + pos * 32 < K);
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        u32x4_t v = xperm8(xv[m][c][e]);
+        if (!valid) v = u32x4_t{0u, 0u, 0u, 0u};
+        s0 = __builtin_amdgcn_fdot2(as_h2(v.x), ones, s0, false);
+        s0 = __builtin_amdgcn_fdot2(as_h2(v.z), ones, s0, false);
+        s1 = __builtin_amdgcn_fdot2(as_h2(v.y), ones, s1, false);
+        s1 = __builtin_amdgcn_fdot2(as_h2(v.w), ones, s1, false);
+        v.y = as_u32(as_h2(v.y) * sixteenth);
+        v.w = as_u32(as_h2(v.w) * sixteenth);
+        xv[m][c][e] = v;
+      }
+      float cs = s0 * 1032.0f + s1 * 72.0f;
+      // sum over the lane quad (j, q = 0..3) that forms one diagonal entry
+      cs += __shfl_xor(cs, 16, 64);
+      cs += __shfl_xor(cs, 32, 64);
+      corr[m][c] = cs;
+    }
+
+  // 5. all rows at once: the RW * NSEG * M_ MFMA chains are interleaved so
+  // their latencies overlap (one wait for the wave's weights).
+  const uint32_t magic = opaque_u32(0x64006400u);
+  float4_t d[M_][RW][NSEG];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int c = 0; c < NSEG; ++c) d[m][r][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int c = 0; c < NSEG; ++c) {
+        const uint32_t w = wv[r][c][e];
+        const uint32_t w8 = w >> 8;
+        u32x4_t b;
+        b.x = and_or(w, 0x000F000Fu, magic);
+        b.y = and_or(w, 0x00F000F0u, magic);
+        b.z = and_or(w8, 0x000F000Fu, magic);
+        b.w = and_or(w8, 0x00F000F0u, magic);
+        const h8 bop = __builtin_bit_cast(h8, b);
+#pragma unroll
+        for (int m = 0; m < M_; ++m)
+          d[m][r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(h8, xv[m][c][e]), bop, d[m][r][c], 0, 0, 0);
+      }
+  }
+  // un-bias and scale every accumulator register, pick the diagonal once
+  float acc[M_][RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    float4_t a4[M_];
+    float ac[M_];
+#pragma unroll
+    for (int m = 0; m < M_; ++m) { a4[m] = float4_t{0.f, 0.f, 0.f, 0.f}; ac[m] = 0.f; }
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      float sc;
+      if constexpr (SD == LQ_F32) sc = sv[r][c];
+      else if constexpr (SD == LQ_F16) sc = float(sv[r][c]);
+      else sc = bf16_to_f32(sv[r][c]);
+      sc = (diag && c * 2048 + pos * 32 < K) ? sc : 0.f;
+#pragma unroll
+      for (int m = 0; m < M_; ++m) {
+        a4[m] += d[m][r][c] * sc;
+        ac[m] += corr[m][c] * sc;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M_; ++m) {
+      const float dv = dreg == 0 ? a4[m][0] : dreg == 1 ? a4[m][1] : dreg == 2 ? a4[m][2] : a4[m][3];
+      acc[m][r] = dv - ac[m];
+    }
+  }
+
+  // 6. reduce each row over the lanes (non-diagonal lanes hold 0)
+#pragma unroll
+  for (int m = 0; m < M_; ++m) {
+    float v[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) v[r] = acc[m][r];
+    int cnt = RW;
+    int width = 32;
+#pragma unroll
+    for (; cnt > 1; cnt >>= 1, width >>= 1) {
+      const bool upper = (lane & width) != 0;
+      const int h = cnt >> 1;
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float keep = upper ? v[i + h] : v[i];
+        const float send = upper ? v[i] : v[i + h];
+        v[i] = keep + __shfl_xor(send, width, 64);
+      }
+    }
+#pragma unroll
+    for (; width > 0; width >>= 1) v[0] += __shfl_xor(v[0], width, 64);
+    int row = 0;
+    {
+      int w2 = 32;
+#pragma unroll
+      for (int c2 = RW; c2 > 1; c2 >>= 1, w2 >>= 1) row = row * 2 + ((lane & w2) ? 1 : 0);
+    }
+    const int lowmask = (64 / RW) - 1;
+    if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+  }
+}
+
+
+// --------------------- decode GEMV, MFMA diagonal, whole 2048-k segments --
+// Same scheme as gemv_diag_kernel, specialised to K % 2048 == 0 with the
+// overhead removed:
+//   * buffer loads (SGPR resource, 32-bit lane offsets, row offset in the
+//     scalar operand); rows past N read as zeros;
+//   * the bias correction is computed by 4 MFMAs per segment (A = the lane's
+//     activations, B = the bias constants 1032 / 1152) and enters each row's
+//     MFMA chain as its initial accumulator (negated), so the chain ends
+//     holding x . (q - 8) directly;
+//   * the diagonal is selected once per (row, segment), scaled, summed.
+template <int M_, int NSEG, int RW, int SD, int OD>
+__global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  typedef typename Elem<SD>::T stype;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * RW;
+  const int half_k = K >> 1;
+  const int j = lane & 15, q = lane >> 4;
+  const int pos = 4 * j + q;
+  const bool diag = q == (j >> 2);
+  const int dreg = j & 3;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<half_t*>(X), 0, M * K * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(W), 0, N * half_k, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(S), 0, N * num_scales * int(sizeof(stype)), 0x00020000);
+
+  // 1. activations (rows m >= M read as zeros): thread t fetches the chunk
+  // lane t / 4 of every wave uses as its operand e = t % 4
+  u32x4_t xv2[M_][NSEG];
+  {
+    const int tl = threadIdx.x >> 2, te = threadIdx.x & 3;
+    const int tpos = 4 * (tl & 15) + (tl >> 4);
+#pragma unroll
+    for (int m = 0; m < M_; ++m)
+#pragma unroll
+      for (int c = 0; c < NSEG; ++c)
+        xv2[m][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+            rx, ((m * K + c * 2048 + tpos * 32 + te * 8) * 2), 0, 0));
+  }
+  // 2. scales
+  uint32_t sv[RW][NSEG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int g = (c * 2048 + pos * 32) / group;
+      if constexpr (sizeof(stype) == 2)
+        sv[r][c] = __builtin_amdgcn_raw_buffer_load_b16(rs, g * 2, ((n0 + r) * num_scales) * 2, 0);
+      else
+        sv[r][c] = __builtin_amdgcn_raw_buffer_load_b32(rs, g * 4, ((n0 + r) * num_scales) * 4, 0);
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. weights
+  u32x4_t wv[RW][NSEG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c)
+      wv[r][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+          rw, c * 1024 + pos * 16, (n0 + r) * half_k, 2 /* nontemporal */));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. activation operands and bias accumulators, built once per workgroup
+  // in LDS: every thread converts M_ * NSEG of the 16-byte chunks (chunk
+  // (m, c, lane, e) -> slot), then waves 0.. compute -bias for one (m, c)
+  // each with 4 MFMAs, then every wave reads its operands back.
+  __shared__ u32x4_t xs_l[M_ * NSEG * 256];
+  __shared__ float4_t nc_l[M_ * NSEG * 64];
+  const half2_t sixteenth = {half_t(0.0625f), half_t(0.0625f)};
+  {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int m = 0; m < M_; ++m)
+#pragma unroll
+      for (int c = 0; c < NSEG; ++c) {
+        // thread t converts the chunk that lane t / 4 uses as its e = t % 4 operand
+        u32x4_t v = xperm8(xv2[m][c]);
+        v.y = as_u32(as_h2(v.y) * sixteenth);
+        v.w = as_u32(as_h2(v.w) * sixteenth);
+        xs_l[(m * NSEG + c) * 256 + t] = v;
+      }
+  }
+  __syncthreads();
+  {
+    const half2_t b1032 = {half_t(1032.f), half_t(1032.f)};
+    const half2_t b1152 = {half_t(1152.f), half_t(1152.f)};
+    u32x4_t bias_w;
+    bias_w.x = as_u32(b1032); bias_w.y = as_u32(b1152); bias_w.z = as_u32(b1032); bias_w.w = as_u32(b1152);
+    const h8 bias_op = __builtin_bit_cast(h8, bias_w);
+    for (int mc = wave; mc < M_ * NSEG; mc += 4) {
+      float4_t cr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(h8, xs_l[mc * 256 + lane * 4 + e]), bias_op, cr, 0, 0, 0);
+      nc_l[mc * 64 + lane] = -cr;
+    }
+  }
+  __syncthreads();
+  u32x4_t xv[M_][NSEG][4];
+  float4_t negcorr[M_][NSEG];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[m][c][e] = xs_l[(m * NSEG + c) * 256 + lane * 4 + e];
+      negcorr[m][c] = nc_l[(m * NSEG + c) * 64 + lane];
+    }
+
+  // 5. rows: decode (5 ops / 8 weights) + MFMA, chains start at -bias
+  const uint32_t magic = opaque_u32(0x64006400u);
+  float acc[M_][RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int m = 0; m < M_; ++m) acc[m][r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      float4_t d[M_];
+#pragma unroll
+      for (int m = 0; m < M_; ++m) d[m] = negcorr[m][c];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = wv[r][c][e];
+        const uint32_t w8 = w >> 8;
+        u32x4_t b;
+        b.x = and_or(w, 0x000F000Fu, magic);
+        b.y = and_or(w, 0x00F000F0u, magic);
+        b.z = and_or(w8, 0x000F000Fu, magic);
+        b.w = and_or(w8, 0x00F000F0u, magic);
+        const h8 bop = __builtin_bit_cast(h8, b);
+#pragma unroll
+        for (int m = 0; m < M_; ++m)
+          d[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xv[m][c][e]), bop,
+                                                        d[m], 0, 0, 0);
+      }
+      float sc;
+      if constexpr (SD == LQ_F32) sc = __uint_as_float(sv[r][c]);
+      else if constexpr (SD == LQ_F16) sc = float(__builtin_bit_cast(half_t, uint16_t(sv[r][c])));
+      else sc = bf16_to_f32(uint16_t(sv[r][c]));
+#pragma unroll
+      for (int m = 0; m < M_; ++m) {
+        const float dv = dreg == 0 ? d[m][0] : dreg == 1 ? d[m][1] : dreg == 2 ? d[m][2] : d[m][3];
+        acc[m][r] += dv * sc;
+      }
+    }
+  }
+
+  // 6. reduce each row over the 16 diagonal lanes
+#pragma unroll
+  for (int m = 0; m < M_; ++m) {
+    float v[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) v[r] = diag ? acc[m][r] : 0.f;
+    int cnt = RW;
+    int width = 32;
+#pragma unroll
+    for (; cnt > 1; cnt >>= 1, width >>= 1) {
+      const bool upper = (lane & width) != 0;
+      const int h = cnt >> 1;
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float keep = upper ? v[i + h] : v[i];
+        const float send = upper ? v[i] : v[i + h];
+        v[i] = keep + __shfl_xor(send, width, 64);
+      }
+    }
+#pragma unroll
+    for (; width > 0; width >>= 1) v[0] += __shfl_xor(v[0], width, 64);
+    int row = 0;
+    {
+      int w2 = 32;
+#pragma unroll
+      for (int c2 = RW; c2 > 1; c2 >>= 1, w2 >>= 1) row = row * 2 + ((lane & w2) ? 1 : 0);
+    }
+    const int lowmask = (64 / RW) - 1;
+    if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+  }
+}
+
+template <int WAVES, int KSPLIT>
+static size_t gemv_lds_bytes(int64_t M, int64_t K, int64_t num_scales, int ssize, int step) {
+  return size_t(M) * (K + 8) * 2 +
+         ((size_t(16 * WAVES / KSPLIT) * num_scales * ssize + 15) & ~size_t(15)) + WAVES * 64 * 16 +
+         size_t((K + step - 1) / step) * 16 * 4;
+}
+
+
+// ------------------------------------------------------------ launchers --
+
+template <int WBITS, int MT, bool POST, int SD, int OD>
+static int launch_skinny_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                           int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const unsigned blocks = unsigned((N + 15) / 16);
+  hipLaunchKernelGGL((skinny_mfma_kernel<WBITS, MT, POST, SD, OD>), dim3(blocks), dim3(kSkThreads),
+                     0, st, static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,
+                     int(M), int(N), int(K), int(K / G), int(G));
+  return check_launch();
+}
+
+
+constexpr int kGvWaves = 8;       // waves per workgroup of the LDS GEMV
+constexpr int kGvMaxLoads = 32;   // weight loads per lane: 32 x 16 B = 128 VGPRs
+
+template <int WBITS, bool POST, int SD, int OD, int KSPLIT, int MAXJ>
+static int launch_gemv_lds_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                             int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  constexpr int rows = 16 * kGvWaves / KSPLIT;
+  const unsigned blocks = unsigned((N + rows - 1) / rows);
+  const size_t lds = gemv_lds_bytes<kGvWaves, KSPLIT>(M, K, K / G, sizeof(typename Elem<SD>::T), SkinnyGeom<WBITS>::kStep);
+  hipLaunchKernelGGL((gemv_lds_kernel<WBITS, POST, SD, OD, kGvWaves, KSPLIT, MAXJ>), dim3(blocks),
+                     dim3(64 * kGvWaves), lds, st, static_cast<const half_t*>(X),
+                     static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K), int(K / G), int(G));
+  return check_launch();
+}
+
+// Split factor for the LDS GEMV: the smallest KSPLIT that keeps each wave
+// within kGvMaxLoads weight loads and yields >= 4096 waves (4 per SIMD on
+// 256 CUs), else the largest; 0 when the problem does not fit the kernel
+// (M > 16, LDS over 64 KB, scale rows not a multiple of 16 bytes).
+static int gemv_lds_split(int64_t M, int64_t N, int64_t K, int64_t G, int step, int ssize) {
+  if (M > 16) return 0;
+  if ((K / G) * ssize % 16 != 0) return 0;
+  if (gemv_lds_bytes<kGvWaves, 1>(M, K, K / G, ssize, step) > 64 * 1024) return 0;
+  const int64_t nsteps = (K + step - 1) / step;
+  for (int ks : {4, 8}) {
+    if ((nsteps + ks - 1) / ks > kGvMaxLoads) continue;
+    const int64_t rows = 16 * kGvWaves / ks;
+    const int64_t waves = (N + rows - 1) / rows * kGvWaves;
+    if (waves >= 4096 || ks == 8) return ks;
+  }
+  return 0;
+}
+
+template <int WBITS, bool POST, int SD, int OD, int KSPLIT>
+static int launch_gemv_lds_j(const void* X, const void* W, const void* S, void* O, int64_t M,
+                             int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int64_t nsteps = (K + SkinnyGeom<WBITS>::kStep - 1) / SkinnyGeom<WBITS>::kStep;
+  const int64_t per_wave = (nsteps + KSPLIT - 1) / KSPLIT;
+  if (per_wave <= 4) return launch_gemv_lds_t<WBITS, POST, SD, OD, KSPLIT, 4>(X, W, S, O, M, N, K, G, st);
+  if (per_wave <= 8) return launch_gemv_lds_t<WBITS, POST, SD, OD, KSPLIT, 8>(X, W, S, O, M, N, K, G, st);
+  if (per_wave <= 16) return launch_gemv_lds_t<WBITS, POST, SD, OD, KSPLIT, 16>(X, W, S, O, M, N, K, G, st);
+  return launch_gemv_lds_t<WBITS, POST, SD, OD, KSPLIT, 32>(X, W, S, O, M, N, K, G, st);
+}
+
+template <int WBITS, bool POST, int SD, int OD>
+static int launch_gemv_lds_p(const void* X, const void* W, const void* S, void* O, int64_t M,
+                             int64_t N, int64_t K, int64_t G, int ks, hipStream_t st) {
+  if (ks == 4) return launch_gemv_lds_j<WBITS, POST, SD, OD, 4>(X, W, S, O, M, N, K, G, st);
+  return launch_gemv_lds_j<WBITS, POST, SD, OD, 8>(X, W, S, O, M, N, K, G, st);
+}
+
+
+template <int M_, int NSEG, int RW, int SD, int OD>
+static int launch_gemv_rows_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                              int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const unsigned blocks = unsigned((N + 4 * RW - 1) / (4 * RW));
+  hipLaunchKernelGGL((gemv_rows_kernel<M_, NSEG, RW, SD, OD>), dim3(blocks), dim3(256), 0, st,
+                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
+                     int(N), int(K), int(K / G), int(G));
+  return check_launch();
+}
+
+template <int M_, int SD, int OD>
+static int launch_gemv_rows_m(const void* X, const void* W, const void* S, void* O, int64_t M,
+                              int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int64_t nseg = (K + 2047) / 2048;
+  if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (nseg <= 2) return launch_gemv_rows_t<M_, 2, 4, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (nseg <= 4) return launch_gemv_rows_t<M_, 4, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+  return launch_gemv_rows_t<M_, 8, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+}
+
+template <int M_, int NSEG, int RW, int SD, int OD>
+static int launch_gemv_diag_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                              int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const unsigned blocks = unsigned((N + 4 * RW - 1) / (4 * RW));
+  hipLaunchKernelGGL((gemv_diag_kernel<M_, NSEG, RW, SD, OD>), dim3(blocks), dim3(256), 0, st,
+                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
+                     int(N), int(K), int(K / G), int(G));
+  return check_launch();
+}
+
+template <int M_, int SD, int OD>
+static int launch_gemv_diag_m(const void* X, const void* W, const void* S, void* O, int64_t M,
+                              int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int64_t nseg = (K + 2047) / 2048;
+  constexpr int rw2 = M_ <= 2 ? 4 : 2;
+  if (nseg <= 1) return launch_gemv_diag_t<M_, 1, rw2 * 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (nseg <= 2) return launch_gemv_diag_t<M_, 2, rw2, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (nseg <= 4) return launch_gemv_diag_t<M_, 4, (rw2 > 1 ? rw2 / 2 : 1), SD, OD>(X, W, S, O, M, N, K, G, st);
+  return launch_gemv_diag_t<M_, 8, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+}
+
+template <int M_, int NSEG, int RW, int SD, int OD>
+static int launch_gemv_seg_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                             int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const unsigned blocks = unsigned((N + 4 * RW - 1) / (4 * RW));
+  hipLaunchKernelGGL((gemv_seg_kernel<M_, NSEG, RW, SD, OD>), dim3(blocks), dim3(256), 0, st,
+                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
+                     int(N), int(K), int(K / G), int(G));
+  return check_launch();
+}
+
+template <int M_, int SD, int OD>
+static int launch_gemv_seg_m(const void* X, const void* W, const void* S, void* O, int64_t M,
+                             int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int64_t nseg = K / 2048;
+  constexpr int rw = M_ <= 2 ? 4 : 2;
+  if (nseg == 1) return launch_gemv_seg_t<M_, 1, rw * 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (nseg == 2) return launch_gemv_seg_t<M_, 2, rw, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (nseg <= 4) return launch_gemv_seg_t<M_, 4, (rw > 2 ? rw / 2 : 1), SD, OD>(X, W, S, O, M, N, K, G, st);
+  return launch_gemv_seg_t<M_, 8, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+}
+
+// The whole-segment kernel: int4, M <= 4, G % 128 == 0, K % 2048 == 0 with
+// K / 2048 in {1, 2, 4, 8}; byte sizes within the buffer-offset range.
+static bool gemv_seg_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G) {
+  const int64_t nseg = K / 2048;
+  return wbits == 4 && M <= 4 && G % 128 == 0 && K % 2048 == 0 &&
+         (nseg == 1 || nseg == 2 || nseg == 4 || nseg == 8) && N * (K / 2) < (int64_t(1) << 31) &&
+         M * K * 2 < (int64_t(1) << 31) && N * (K / G) * 4 < (int64_t(1) << 31);
+}
+
+// The diagonal-MFMA kernel applies to int4, M <= 4, G % 128 == 0, K <= 16384.
+static bool gemv_diag_ok(int wbits, int64_t M, int64_t K, int64_t G) {
+  return wbits == 4 && M <= 4 && G % 128 == 0 && K % 128 == 0 && K <= 16384 && K >= 128;
+}
+
+// The row-contiguous kernel applies to int4, M <= 2, K % 32 == 0, G % 32 == 0,
+// K <= 16384.
+static bool gemv_rows_ok(int wbits, int64_t M, int64_t K, int64_t G) {
+  return wbits == 4 && M <= 2 && K % 32 == 0 && G % 32 == 0 && K <= 16384 && K >= 32;
+}
+
+template <int WBITS, int MT, int SD, int OD>
+static int launch_skinny_mt(const void* X, const void* W, const void* S, void* O, int64_t M,
+                            int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  if (G % SkinnyGeom<WBITS>::kStep == 0)
+    return launch_skinny_t<WBITS, MT, true, SD, OD>(X, W, S, O, M, N, K, G, st);
+  return launch_skinny_t<WBITS, MT, false, SD, OD>(X, W, S, O, M, N, K, G, st);
+}
+
+template <int WBITS, int SD, int OD>
+static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void* O, int64_t M,
+                               int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  if constexpr (WBITS == 4 && SD != LQ_BF16 && OD != LQ_BF16) {
+    if (gemv_seg_ok(WBITS, M, N, K, G)) {
+      if (M == 1) return launch_gemv_seg_m<1, SD, OD>(X, W, S, O, M, N, K, G, st);
+      if (M == 2) return launch_gemv_seg_m<2, SD, OD>(X, W, S, O, M, N, K, G, st);
+      return launch_gemv_seg_m<4, SD, OD>(X, W, S, O, M, N, K, G, st);
+    }
+    if (gemv_diag_ok(WBITS, M, K, G)) {
+      if (M == 1) return launch_gemv_diag_m<1, SD, OD>(X, W, S, O, M, N, K, G, st);
+      if (M == 2) return launch_gemv_diag_m<2, SD, OD>(X, W, S, O, M, N, K, G, st);
+      return launch_gemv_diag_m<4, SD, OD>(X, W, S, O, M, N, K, G, st);
+    }
+    if (gemv_rows_ok(WBITS, M, K, G)) {
+      if (M == 1) return launch_gemv_rows_m<1, SD, OD>(X, W, S, O, M, N, K, G, st);
+      return launch_gemv_rows_m<2, SD, OD>(X, W, S, O, M, N, K, G, st);
+    }
+  }
+  const int ks = (SD != LQ_BF16 && OD != LQ_BF16)
+                     ? gemv_lds_split(M, N, K, G, SkinnyGeom<WBITS>::kStep, sizeof(typename Elem<SD>::T))
+                     : 0;
+  if constexpr (SD != LQ_BF16 && OD != LQ_BF16) if (ks) {
+    if (G % SkinnyGeom<WBITS>::kStep == 0)
+      return launch_gemv_lds_p<WBITS, true, SD, OD>(X, W, S, O, M, N, K, G, ks, st);
+    return launch_gemv_lds_p<WBITS, false, SD, OD>(X, W, S, O, M, N, K, G, ks, st);
+  }
+  if (M <= 16) return launch_skinny_mt<WBITS, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (M <= 32) return launch_skinny_mt<WBITS, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+  return launch_skinny_mt<WBITS, 4, SD, OD>(X, W, S, O, M, N, K, G, st);
+}
+
+template <int WBITS>
+int launch_skinny(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                  int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+#define LQ_SK(SD_, OD_) \
+  if (sd == SD_ && od == OD_) return launch_skinny_sd_od<WBITS, SD_, OD_>(X, W, S, O, M, N, K, G, st)
+  LQ_SK(LQ_F16, LQ_F16);
+  LQ_SK(LQ_F16, LQ_F32);
+  LQ_SK(LQ_F16, LQ_BF16);
+  LQ_SK(LQ_F32, LQ_F16);
+  LQ_SK(LQ_F32, LQ_F32);
+  LQ_SK(LQ_F32, LQ_BF16);
+  LQ_SK(LQ_BF16, LQ_F16);
+  LQ_SK(LQ_BF16, LQ_F32);
+  LQ_SK(LQ_BF16, LQ_BF16);
+#undef LQ_SK
+  return LQ_ERR_DTYPE;
+}
+
+}  // namespace lq

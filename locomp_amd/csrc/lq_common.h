@@ -103,6 +103,66 @@ __device__ __forceinline__ void int8x4_to_h2(uint32_t w, half2_t out[2]) {
   out[1] = as_h2(hi) - off;
 }
 
+
+// ------------------------------------ biased, k-permuted unpack (MFMA B) --
+// For MFMA consumers the order of k inside an 8-wide group is free as long as
+// the A operand uses the same order.  These helpers emit, for one group of 8
+// weights k0..k7, the four half2 (k0,k4), (k1,k5), (k2,k6), (k3,k7) *biased*:
+// each half is the fp16 value BIAS + q exactly, with BIAS = 1032 for int4
+// (1024 + q, q = 0..15, stands for q - 8) and 1152 for int8 (1024 + (b ^ 0x80)
+// stands for b).  Callers subtract BIAS * sum(x) once per k-range instead of
+// once per weight.  xperm8 applies the same permutation to 8 activations.
+
+// (x & mask) | orv.  Written in C (not inline asm) so the compiler's hazard
+// tracking sees the VALU write when the result feeds an MFMA; `orv` should be
+// an opaque_u32 value so the pair is selected as one v_and_or_b32 (mask in an
+// SGPR, orv in a VGPR) rather than v_and + v_or with two literals.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t orv) {
+  return (x & mask) | orv;
+}
+
+// A value the optimiser cannot constant-fold (held in a VGPR).
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+  __asm__ volatile("" : "+v"(v));
+  return v;
+}
+
+constexpr float kInt4Bias = 1032.0f;
+constexpr float kInt8Bias = 1152.0f;
+
+// int4: one dword = 8 weights.  (w >> 4i) & 0x000F000F puts nibble i of byte 0
+// (k = i) in bits 3:0 and nibble i of byte 2 (k = i + 4) in bits 19:16.
+__device__ __forceinline__ u32x4_t int4x8_biased_kperm(uint32_t w) {
+  const uint32_t magic = opaque_u32(0x64006400u);
+  u32x4_t r;
+  r.x = and_or(w, 0x000F000Fu, magic);         // (k0, k4)
+  r.y = and_or(w >> 4, 0x000F000Fu, magic);    // (k1, k5)
+  r.z = and_or(w >> 8, 0x000F000Fu, magic);    // (k2, k6)
+  r.w = and_or(w >> 12, 0x000F000Fu, magic);   // (k3, k7)
+  return r;
+}
+
+// int8: two dwords = 8 weights.  Pair i takes byte i of each dword; the xor
+// flips the sign bit (b + 128) and writes the 0x64 exponent byte at once.
+__device__ __forceinline__ u32x4_t int8x8_biased_kperm(uint32_t w0, uint32_t w1) {
+  u32x4_t r;
+  r.x = __builtin_amdgcn_perm(w1, w0, 0x0C040C00u) ^ 0x64806480u;
+  r.y = __builtin_amdgcn_perm(w1, w0, 0x0C050C01u) ^ 0x64806480u;
+  r.z = __builtin_amdgcn_perm(w1, w0, 0x0C060C02u) ^ 0x64806480u;
+  r.w = __builtin_amdgcn_perm(w1, w0, 0x0C070C03u) ^ 0x64806480u;
+  return r;
+}
+
+// 8 fp16 activations x0..x7 (4 dwords) -> (x0,x4), (x1,x5), (x2,x6), (x3,x7).
+__device__ __forceinline__ u32x4_t xperm8(u32x4_t d) {
+  u32x4_t r;
+  r.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
+  r.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
+  r.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
+  r.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+  return r;
+}
+
 // ---------------------------------------------------------------- launch --
 
 __host__ __forceinline__ int check_launch() {
