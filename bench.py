@@ -177,6 +177,38 @@ def cpu_baseline(case, budget_s=20.0):
     }
 
 
+def profile_case(name, launches=50):
+    """Eager launches of one configuration (rotating replicas), for rocprofv3.
+
+    "copy" copies a 64 MiB device buffer (torch copy_): its FETCH_SIZE /
+    WRITE_SIZE per dispatch calibrate the counters against known bytes."""
+    import torch
+    from locomp_amd import synth
+    s = torch.cuda.current_stream()
+    if name == "copy":
+        a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(launches):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print("copy: 67108864 bytes read + 67108864 written per dispatch")
+        return 0
+    c3, c2, c4, c5 = synth.CFG3, synth.CFG2, synth.CFG4, synth.CFG5A
+    case = {
+        "gemv": lambda: Case("matvec", 4, 1, c3["N"], c3["K"], c3["G"], c3["lo"], c3["hi"]),
+        "gemv_m16": lambda: Case("matvec", 4, 16, c3["N"], c3["K"], c3["G"], c3["lo"], c3["hi"]),
+        "gemm": lambda: Case("matvec", 4, c5["M"], c5["N"], c5["K"], c5["G"], c5["lo"], c5["hi"],
+                             min_bytes=0, max_replicas=4),
+        "dequant": lambda: Case("dequant", 4, 0, c2["N"], c2["K"], c2["G"], c2["lo"], c2["hi"]),
+        "w8a16": lambda: Case("matvec", 8, c4["M"], c4["N"], c4["K"], c4["G"], c4["lo"], c4["hi"]),
+    }[name]()
+    for i in range(launches):
+        case.launch(i, ctypes.c_void_p(s.cuda_stream))
+    torch.cuda.synchronize()
+    print(f"{name}: {launches} launches, {case.algo_bytes} algorithmic bytes per launch")
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,6 +216,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra cases to run (default all)")
+    ap.add_argument("--profile", default="", choices=["", "gemv", "gemv_m16", "gemm", "dequant", "w8a16", "copy"],
+                    help="launch one case 50 times eagerly and exit (for rocprofv3 counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -195,6 +229,9 @@ def main():
         print("no HIP device visible", file=sys.stderr)
         return 1
     from locomp_amd import synth
+
+    if args.profile:
+        return profile_case(args.profile)
 
     c3 = synth.CFG3
     log("case gemv_w4a16 M=1")
@@ -243,6 +280,11 @@ def main():
                  Case("matvec", 8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm")
 
     cpu = None if args.no_cpu else cpu_baseline(head)
+    traffic = None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_w4a16_m1_traffic.json")
+    if os.path.exists(tpath):   # HBM bytes per launch from the committed rocprofv3 PMC passes
+        with open(tpath) as f:
+            traffic = int(json.load(f)["traffic_bytes"])
 
     line = {
         "metric": METRIC,
@@ -261,7 +303,7 @@ def main():
                                "fp32 accumulate", "M": 1, "K": 4096, "N": 11008, "group": 128,
                    "weight_replicas": head.R},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": head.algo_bytes,
                      "avg_launch_us": round(us, 3)},
         "cpu_baseline": cpu,

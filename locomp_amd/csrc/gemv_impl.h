@@ -1,24 +1,24 @@
 #pragma once
-// Decode-shaped dequant-matmul (M <= 64) for gfx950, and the shape-generic
-// fallback used for every case the fast kernels do not cover.
+// Decode-shaped dequant-matmul kernels (M <= 64) for gfx950.  Included by
+// gemv_w4.hip / gemv_w8.hip, which instantiate launch_skinny<WBITS>.
 //
 // Reference semantics: locomp examples/38_quantized_matmul.py:30-87 (int4)
 // and :94-134 (int8): O[m, n] = sum_k X[m, k] * w[n, k], fp32 accumulation.
 //
-// Fast kernel ("skinny"): fp16 activations, CDNA4 v_mfma_f32_16x16x32_f16.
-//   * A workgroup of 4 waves owns 16 weight rows and all M; the 4 waves split
-//     K (wave w takes k-steps w, w+4, ...) and their partial 16x(16*MT)
-//     tiles are summed through LDS at the end.
-//   * Lane l = (n = l % 16, quarter = l / 16) loads 16 packed bytes of row n
-//     per k-step with one 128-bit load; a wave instruction therefore covers
-//     16 rows x 64 contiguous bytes, and the 4 waves together stream 256
-//     contiguous bytes of every row.  Weights are touched exactly once.
-//   * The 16 bytes are dequantised in registers to exact fp16 (q - 8) (int4)
-//     or q (int8) and fed to the MFMA B operand as-is; the MFMA's K order is
-//     the same for A and B, so lane l's A operand is X[m = l % 16, same k].
-//   * Scales: when every k-step lies in one group (G % step == 0) the step's
-//     MFMA result is multiplied by s[n, g] in fp32 ("post-scale"); otherwise
-//     B is multiplied by its lane's scale in fp16 before the MFMA.
+// Kernel choice (launch_skinny_sd_od, fp16 activations):
+//   gemv_seg_kernel   int4, M <= 4, G % 128 == 0, K % 2048 == 0   (headline)
+//   gemv_diag_kernel  int4, M <= 4, G % 128 == 0, K % 128 == 0
+//   gemv_rows_kernel  int4, M <= 2, G % 32 == 0
+//   gemv_lds_kernel   M <= 16, activations + scales staged in LDS
+//   skinny_mfma_kernel  M <= 64 (and everything the above reject)
+//
+// skinny_mfma_kernel: a workgroup of 4 waves owns 16 weight rows and all M;
+// the waves split K (wave w takes k-steps w, w+4, ...) and reduce through
+// LDS.  Lane l = (n = l % 16, quarter = l / 16) loads 16 packed bytes of row
+// n per k-step; the bytes are dequantised in registers to exact fp16 and fed
+// to the MFMA B operand; the MFMA's K order is the same for A and B, so lane
+// l's A operand is X[m = l % 16, same k].  Scales: post-scale in fp32 when a
+// k-step lies in one group, else the B operand is scaled in fp16.
 #include "lq_common.h"
 
 namespace lq {
