@@ -29,9 +29,15 @@ FLAGS = [
 ]
 
 
+# Per-source extra flags.  gemm.hip: select the VGPR-destination MFMA form;
+# with AGPR destinations the allocator does not tie each MFMA's accumulator
+# input to its output and copies accumulators between VGPRs and AGPRs.
+EXTRA = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str) -> Path:
     obj = OBJDIR / (Path(src).stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

@@ -5,163 +5,317 @@
 // activation row (locomp examples/38_quantized_matmul.py:154).  Values follow
 // the same definition: w = (q - 8) * s[n, k / G].
 //
-// Tiling: a 256-lane workgroup owns a BM x BN output tile and walks K in BK
-// steps.  Per step, X[BM, BK] is copied to LDS as-is and the packed weights
-// W[BN, BK/2] are loaded (one 128-bit load per lane = 32 k of one row),
-// dequantised in registers to fp16 (q - 8) * s (exact (q - 8), one rounding
-// of the product) and written to LDS, so each weight is dequantised once
-// per workgroup.  LDS is double-buffered: the global loads for step t + 1 are
-// issued before the MFMAs of step t.  Four waves in a 2 x 2 arrangement each
-// compute a (BM/2) x (BN/2) sub-tile with v_mfma_f32_16x16x32_f16.
+// Tiling (default GemmCfg<8, 1, 2, 8>: 512 lanes, BM x BN = 256 x 128, BK = 64):
+//   * Wave w owns output rows [32 w, 32 w + 32) and all 128 columns: 2 x 8
+//     tiles of v_mfma_f32_16x16x32_f16 (fp32 accumulators in VGPRs).
+//   * Activations: each k-step's 256 x 64 fp16 tile is copied global -> LDS by
+//     the gfx950 direct-to-LDS load (global_load_lds_dwordx4): no VGPRs, 128 B
+//     of one row per 8 lanes, XOR-swizzled chunk order chosen through the
+//     source addresses.  A 3-slot ring keeps steps ks + 1 and ks + 2 in flight.
+//   * Weights: the packed 128 x 32-byte tile of step ks + 2 is loaded into
+//     registers during step ks, dequantised during step ks + 1 to exact fp16
+//     (q - 8) times the fp16 scale (one rounding) and written to an
+//     XOR-swizzled LDS tile (2 stages) that every wave reads as the B operand.
+//   * One barrier per step.  The loop's loads are inline asm with hand-placed
+//     s_waitcnt (the compiler would drain vmcnt before every LDS read after an
+//     LDS-DMA); MFMAs use the VGPR-destination form (build flag), which keeps
+//     the accumulators from being copied between VGPRs and AGPRs.
+//   * XCD-aware order: consecutive workgroups are dealt round-robin to the 8
+//     XCDs, so the tile sequence is arranged for each XCD to walk one 256-row
+//     block of X (2 MB at K = 4096: it stays in that XCD's 4 MB L2).
+#include <type_traits>
+
 #include "lq_common.h"
+
+#ifndef LQ_GEMM_VARIANT
+#define LQ_GEMM_VARIANT 2
+#endif
 
 namespace lq {
 
-constexpr int kGmThreads = 256;
-constexpr int kBM = 128;
-constexpr int kBN = 128;
-constexpr int kBK = 64;
-constexpr int kLdsStride = kBK + 8;  // halves; 144-byte rows spread ds_read_b128 over banks
-constexpr int kWM = kBM / 2;          // wave tile
-constexpr int kWN = kBN / 2;
-constexpr int kTM = kWM / 16;         // 16x16 MFMA tiles per wave
-constexpr int kTN = kWN / 16;
-
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
-template <int SD, int OD>
-__global__ __launch_bounds__(kGmThreads, 2) void gemm_w4_kernel(
+constexpr int kBK = 64;
+
+// Tile configuration: WM x WN waves, each owning (16 TM) x (16 TN) outputs.
+template <int WM_, int WN_, int TM_, int TN_>
+struct GemmCfg {
+  static constexpr int WM = WM_, WN = WN_, TM = TM_, TN = TN_;
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int BM = WM * TM * 16;
+  static constexpr int BN = WN * TN * 16;
+  // packed weight bytes per step: BN rows x 32 bytes; bytes per loader thread
+  static constexpr int kBBytes = BN * 32 / kThreads;
+  static_assert(kBBytes == 4 || kBBytes == 8 || kBBytes == 16, "B loader granularity");
+};
+
+// LDS element offset (halves) of 16-byte chunk c (of 8 per row) of weight
+// row n, XOR-swizzled so the 16 rows one ds_read_b128 touches spread over banks.
+__device__ __forceinline__ int b_lds_off(int n, int c) { return n * kBK + ((c ^ (n & 7)) << 3); }
+
+// ------------------------------------------------------ explicit loads --
+// The main loop's global loads are issued with inline asm so that the
+// compiler's wait analysis (which treats an LDS-DMA as a write to all of LDS
+// and would drain vmcnt before every LDS read) stays out of the loop; every
+// wait is placed by hand and names the registers it guards, so no consumer
+// can be scheduled before it.  M0 is used by nothing else in this kernel.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// 16 bytes per lane from global memory to LDS (lane L -> lds + 16 L).
+__device__ __forceinline__ void dma16(const void* g, const void* lds) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  __asm__ volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                   :: "v"(g), "s"(a) : "memory", "m0");
+}
+__device__ __forceinline__ u32x4_t gload_b128(const void* g) {
+  u32x4_t v;
+  __asm__ volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+__device__ __forceinline__ u32x2_t gload_b64(const void* g) {
+  u32x2_t v;
+  __asm__ volatile("global_load_dwordx2 %0, %1, off nt" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t gload_u16(const void* g) {
+  uint32_t v;
+  __asm__ volatile("global_load_ushort %0, %1, off" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t gload_b32(const void* g) {
+  uint32_t v;
+  __asm__ volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+
+// A (activation) tile in LDS: BM rows x 64 k fp16 = 128 B per row, 16-byte
+// chunk c of row m stored at chunk position c ^ (m & 7).
+__device__ __forceinline__ int a_lds_off(int m, int c) { return m * kBK + ((c ^ (m & 7)) << 3); }
+
+constexpr int kAStages = 3;   // activation ring: steps ks, ks + 1, ks + 2
+constexpr int kBStages = 2;
+
+template <class C, int SD, int OD>
+__global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
-    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
-  __shared__ __attribute__((aligned(16))) half_t As[2][kBM * kLdsStride];
-  __shared__ __attribute__((aligned(16))) half_t Bs[2][kBN * kLdsStride];
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group, int tiles_m, int tiles_n) {
+  constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN;
+  static_assert(BM % (8 * C::kWaves) == 0, "A DMA: whole 1 KB instructions per wave");
+  typedef typename Elem<SD>::T stype;
+  __shared__ __attribute__((aligned(16))) half_t As[kAStages][BM * kBK];
+  __shared__ __attribute__((aligned(16))) half_t Bs[kBStages][BN * kBK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
   const int r16 = lane & 15;
   const int q4 = lane >> 4;
+  const int wm = wave / C::WN;
+  const int wn = wave % C::WN;
 
-  const int m0 = blockIdx.y * kBM;
-  const int n0 = blockIdx.x * kBN;
+  // XCD-aware tile order: workgroup b runs on XCD b % 8; XCD x takes the
+  // contiguous slice [x * per, (x + 1) * per) of the row-major tile list.
+  const int total = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if (total % 8 == 0) t = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+  const int m0 = (t / tiles_n) * BM;
+  const int n0 = (t % tiles_n) * BN;
   const int half_k = K >> 1;
+  const int wrow0 = wm * TM * 16;              // first tile row this wave multiplies
 
-  // Global -> register assignment.
-  // A: 4 chunks of 16 B per lane; chunk j covers row (tid / 8) + 32 j, halves (tid % 8) * 8.
-  const int a_row = tid >> 3;
-  const int a_col = (tid & 7) * 8;
-  // B: row tid / 2, packed bytes (tid % 2) * 16 .. +16 (= 32 k).
-  const int b_row = tid >> 1;
-  const int b_half = tid & 1;
-  const int bn = n0 + b_row;
-  const bool b_ok = bn < N;
-  const uint8_t* wrow = W + size_t(b_ok ? bn : 0) * half_k;
-
-  u32x4_t a_reg[4];
-  u32x4_t b_reg;
-  float b_scale = 0.f;
-
-  auto load_tile = [&](int kt) {
-    const int k0 = kt * kBK;
+  // A DMA: wave w copies rows [w * kDmaRows, (w + 1) * kDmaRows) of the tile
+  // (128 B per row): instruction i writes LDS bytes [i KB, i KB + 1 KB) of that
+  // slice, lane L at +16 L, i.e. row (8 i + L / 8), chunk position L % 8,
+  // holding logical chunk (L % 8) ^ (row & 7).  Eight lanes cover one row.
+  constexpr int kDmaRows = BM / C::kWaves;
+  constexpr int kADma = kDmaRows / 8;
+  const int drow0 = wave * kDmaRows;
+  const half_t* adma_src[kADma];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + a_row + 32 * j;
-      if (m < M)
-        a_reg[j] = *reinterpret_cast<const u32x4_t*>(X + size_t(m) * K + k0 + a_col);
-      else
-        a_reg[j] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-    const int kb = k0 + b_half * 32;
-    if (b_ok) {
-      b_reg = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + (kb >> 1)));
-      b_scale = load_f32<SD>(S, size_t(bn) * num_scales + kb / group);
-    } else {
-      b_reg = u32x4_t{0u, 0u, 0u, 0u};
-      b_scale = 0.f;
-    }
+  for (int i = 0; i < kADma; ++i) {
+    const int row = drow0 + 8 * i + (lane >> 3);
+    const int m = min(m0 + row, M - 1);
+    const int c = (lane & 7) ^ (row & 7);
+    adma_src[i] = X + size_t(m) * K + c * 8;
+  }
+  auto dma_a = [&](int stage, int k0) {
+#pragma unroll
+    for (int i = 0; i < kADma; ++i)
+      dma16(adma_src[i] + k0, &As[stage][(drow0 + 8 * i) * kBK]);
   };
 
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<u32x4_t*>(&As[buf][(a_row + 32 * j) * kLdsStride + a_col]) = a_reg[j];
-    const half_t hs = half_t(b_scale);
+  // B loader: C::kBBytes packed bytes (2 k per byte) of one weight row
+  constexpr int kPerRow = 32 / C::kBBytes;
+  const int b_n = tid / kPerRow;
+  const int b_part = tid % kPerRow;
+  const int bn = min(n0 + b_n, N - 1);
+  const uint8_t* wrow = W + size_t(bn) * half_k + b_part * C::kBBytes;
+  const stype* sp = static_cast<const stype*>(S) + size_t(bn) * num_scales;
+  static_assert(C::kBBytes == 16 || C::kBBytes == 8, "64- or 128-bit weight loads");
+  constexpr int kBWords = C::kBBytes / 4;
+  // Packed weights: `bfar` receives the loads of step ks + 2 during step ks;
+  // at the end of the step (after its wait) they move to `bnear`, which the
+  // next step dequantises while its MFMAs run.
+  u32x4_t bfar, bnear;    // 16-byte loads (bnear also holds the 8-byte case)
+  u32x2_t bfar2;          // 8-byte loads
+  uint32_t sfar, snear;   // raw scale bits, converted when the tile is dequantised
+
+  auto load_b = [&](int k0) {
+    if constexpr (kBWords == 4) bfar = gload_b128(wrow + (k0 >> 1));
+    else bfar2 = gload_b64(wrow + (k0 >> 1));
+    const stype* ps = sp + (k0 + b_part * C::kBBytes * 2) / group;
+    if constexpr (sizeof(stype) == 2) sfar = gload_u16(ps);
+    else sfar = gload_b32(ps);
+  };
+  // WAIT_FAR(n): wait until at most n loads are outstanding; ties the `far`
+  // registers so their consumers (and the copy to `near`) stay below it.  A
+  // register written by an asm load must not be read (or copied) before this.
+#define WAIT_FAR(n)                                                                         \
+  do {                                                                                      \
+    if constexpr (kBWords == 4)                                                             \
+      __asm__ volatile("s_waitcnt vmcnt(%2)" : "+v"(bfar), "+v"(sfar) : "n"(n) : "memory"); \
+    else                                                                                    \
+      __asm__ volatile("s_waitcnt vmcnt(%2)" : "+v"(bfar2), "+v"(sfar) : "n"(n) : "memory");\
+  } while (0)
+#define FAR_TO_NEAR()                                                      \
+  do {                                                                     \
+    if constexpr (kBWords == 4) bnear = bfar;                              \
+    else bnear = u32x4_t{bfar2.x, bfar2.y, 0u, 0u};                        \
+    snear = sfar;                                                          \
+  } while (0)
+  auto store_b = [&](int stage) {
+    float bs;
+    if constexpr (SD == LQ_F32) bs = __uint_as_float(snear);
+    else if constexpr (SD == LQ_F16) bs = float(__builtin_bit_cast(half_t, uint16_t(snear)));
+    else bs = bf16_to_f32(uint16_t(snear));
+    const uint32_t bq[4] = {bnear.x, bnear.y, bnear.z, bnear.w};   // first kBWords used
+    const half_t hs = half_t(bs);
     const half2_t s2 = {hs, hs};
-    half_t* dst = &Bs[buf][b_row * kLdsStride + b_half * 32];
+    half_t* dst = Bs[stage];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kBWords; ++i) {
       half2_t h[4];
-      int4x8_to_h2(b_reg[i], h);
+      int4x8_to_h2(bq[i], h);
       u32x4_t v;
       v.x = as_u32(h[0] * s2);
       v.y = as_u32(h[1] * s2);
       v.z = as_u32(h[2] * s2);
       v.w = as_u32(h[3] * s2);
-      *reinterpret_cast<u32x4_t*>(dst + i * 8) = v;
+      *reinterpret_cast<u32x4_t*>(dst + b_lds_off(b_n, b_part * kBWords + i)) = v;
     }
   };
 
-  float4_t acc[kTM][kTN];
+  float4_t acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < kTM; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int ktiles = K / kBK;
-  load_tile(0);
-  store_tile(0);
+  const int ksteps = K / kBK;
+  // prologue: A(0), A(1) by DMA; B(0) dequantised into LDS; B(1) in `near`
+  dma_a(0, 0);
+  dma_a(1, min(1, ksteps - 1) * kBK);
+  load_b(0);
+  WAIT_FAR(0);
+  FAR_TO_NEAR();
+  store_b(0);
+  load_b(min(1, ksteps - 1) * kBK);
+  WAIT_FAR(0);
+  FAR_TO_NEAR();
   __syncthreads();
 
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ktiles) load_tile(kt + 1);
-    const half_t* as = As[cur];
-    const half_t* bs = Bs[cur];
+  int a_stage = 0;
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const int b_stage = ks & 1;
+    const int a_next2 = a_stage == 0 ? 2 : a_stage - 1;   // (a_stage + 2) % 3
+    // Issue B(ks + 2) then A(ks + 2) (branch-free: past the end they re-read
+    // the last step and land in buffers no one reads).
+    const int k2 = min(ks + 2, ksteps - 1) * kBK;
+    load_b(k2);
+    dma_a(a_next2, k2);
+    const half_t* as_l = As[a_stage];
+    const half_t* bs_l = Bs[b_stage];
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += 32) {
-      h8 a[kTM], b[kTN];
+    for (int kk = 0; kk < 2; ++kk) {
+      h8 b[TN];
 #pragma unroll
-      for (int i = 0; i < kTM; ++i)
-        a[i] = *reinterpret_cast<const h8*>(as + (wm * kWM + i * 16 + r16) * kLdsStride + kk + q4 * 8);
+      for (int j = 0; j < TN; ++j)
+        b[j] = *reinterpret_cast<const h8*>(bs_l + b_lds_off((wn * TN + j) * 16 + r16, kk * 4 + q4));
 #pragma unroll
-      for (int j = 0; j < kTN; ++j)
-        b[j] = *reinterpret_cast<const h8*>(bs + (wn * kWN + j * 16 + r16) * kLdsStride + kk + q4 * 8);
+      for (int i = 0; i < TM; ++i) {
+        const h8 a = *reinterpret_cast<const h8*>(as_l + a_lds_off(wrow0 + i * 16 + r16, kk * 4 + q4));
 #pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int j = 0; j < kTN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], acc[i][j], 0, 0, 0);
+      }
     }
-    if (kt + 1 < ktiles) store_tile(cur ^ 1);
+#if LQ_GEMM_VARIANT == 1
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+    store_b(b_stage ^ 1);                      // dequantise B(ks + 1)
+#if LQ_GEMM_VARIANT == 0
+    // Interleave that VALU / LDS-write work between the MFMAs.
+#pragma unroll
+    for (int g = 0; g < 32; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // 2 VALU
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+#elif LQ_GEMM_VARIANT == 3
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // 4 VALU
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+#endif
+    WAIT_FAR(kADma);                           // B(ks + 2) and A(ks + 1) landed
+    FAR_TO_NEAR();
     __syncthreads();
+    a_stage = a_stage == 2 ? 0 : a_stage + 1;
   }
 
-  // Epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile.
+#undef WAIT_FAR
+#undef FAR_TO_NEAR
+  // Epilogue: lane holds rows 4 * (lane / 16) + r, column lane % 16 of each tile.
 #pragma unroll
-  for (int i = 0; i < kTM; ++i) {
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const int n = n0 + wn * kWN + j * 16 + r16;
-      if (n >= N) continue;
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + wrow0 + i * 16 + q4 * 4 + r;
+      if (m >= M) continue;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * kWM + i * 16 + q4 * 4 + r;
-        if (m < M) store_f32<OD>(O, size_t(m) * N + n, acc[i][j][r]);
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + (wn * TN + j) * 16 + r16;
+        if (n < N) store_f32<OD>(O, size_t(m) * N + n, acc[i][j][r]);
       }
     }
   }
 }
 
+#ifndef LQ_GEMM_CFG
+#define LQ_GEMM_CFG 8, 1, 2, 8
+#endif
+typedef GemmCfg<LQ_GEMM_CFG> GemmDefault;   // default: 256 x 128 tile, 8 waves of 32 x 128
+
+template <class C, int SD, int OD>
+static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O, int64_t M,
+                           int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int tiles_m = int((M + C::BM - 1) / C::BM);
+  const int tiles_n = int((N + C::BN - 1) / C::BN);
+  hipLaunchKernelGGL((gemm_w4_kernel<C, SD, OD>), dim3(unsigned(tiles_m * tiles_n)),
+                     dim3(C::kThreads), 0, st, static_cast<const half_t*>(X),
+                     static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K), int(K / G),
+                     int(G), tiles_m, tiles_n);
+  return check_launch();
+}
+
 template <int SD, int OD>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, hipStream_t st) {
-  dim3 grid(unsigned((N + kBN - 1) / kBN), unsigned((M + kBM - 1) / kBM));
-  hipLaunchKernelGGL((gemm_w4_kernel<SD, OD>), grid, dim3(kGmThreads), 0, st,
-                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
-                     int(N), int(K), int(K / G), int(G));
-  return check_launch();
+  return launch_gemm_cfg<GemmDefault, SD, OD>(X, W, S, O, M, N, K, G, st);
 }
 
 template <int WBITS>
