@@ -107,6 +107,48 @@ class Case:
         return self.O[0].cpu().numpy()
 
 
+class Stack:
+    """SmolLM2-135M-shaped decode linear stack: 30 layers x 7 int4 g32 GEMVs
+    (q, k, v, o, gate, up, down) at M = 1, random weights (BASELINE config 5b).
+    One step = all 210 GEMVs of one token, launched back to back (in a graph)."""
+
+    def __init__(self, seed=0, G=32, fused=False):
+        """fused=True concatenates the weights of linears that read the same
+        activation (q|k|v: N = 960, gate|up: N = 3072): 4 GEMVs per layer."""
+        import torch
+        from locomp_amd import synth, _lib
+        self.lib = _lib.load()
+        rng = np.random.default_rng(seed)
+        self.layers = []
+        self.algo_bytes = 0
+        xs = {}
+        for K in (576, 1536):
+            xs[K] = _dev(synth.activations(rng, 1, K))
+        self.xs = xs
+        shapes = synth.SMOLLM2_LAYER
+        if fused:
+            (nq, k0), (nk, _), (nv, _), o, (ng, _), (nu, _), down = shapes
+            shapes = [(nq + nk + nv, k0), o, (ng + nu, k0), down]
+        for _ in range(synth.SMOLLM2_LAYERS):
+            for (N, K) in shapes:
+                W = synth.int4_weights(rng, N, K)
+                S = synth.scales(rng, N, K // G, 0.001, 0.01)
+                O = torch.empty(N, dtype=torch.float16, device="cuda")
+                self.layers.append((N, K, G, _dev(W), _dev(S), O))
+                self.algo_bytes += W.nbytes + S.nbytes + K * 2 + N * 2
+        self.R = 1
+        torch.cuda.synchronize()
+
+    def launch(self, i, stream):
+        vp = ctypes.c_void_p
+        for (N, K, G, W, S, O) in self.layers:
+            rc = self.lib.locomp_amd_dequant_matvec_int4(
+                vp(self.xs[K].data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
+                K, K // 2, K // G, G, N, 1, 1, 1, 1, stream)
+            if rc != 0:
+                raise RuntimeError(f"launch failed: {rc}")
+
+
 def time_graph(case, steps, warmup, per_graph=None):
     """Capture `per_graph` launches in a graph; replay to cover warmup + steps.
 
@@ -274,6 +316,17 @@ def main():
         c = synth.CFG2
         run_case("dequant_int4_4096x4096_g32_f16",
                  Case("dequant", 4, 0, c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm")
+    if want("smollm2"):
+        for fused in (False, True):
+            st = Stack(fused=fused)
+            tt, nn = time_graph(st, 40, 5, per_graph=4)
+            per = tt / nn
+            d = {"us_per_token": round(per * 1e6, 2), "GB_s": round(st.algo_bytes / per / 1e9, 1),
+                 "gemvs_per_token": len(st.layers), "algorithmic_bytes": st.algo_bytes,
+                 "us_per_gemv": round(per * 1e6 / len(st.layers), 3)}
+            name = "smollm2_135m_int4_g32_decode_stack" + ("_qkv_gateup_fused" if fused else "")
+            extra[name] = d
+            log(name, d)
     if want("w8a16"):
         c = synth.CFG4
         run_case("w8a16_M64_14336x4096",

@@ -219,3 +219,12 @@ def test_all_q8_gives_zero(M, K):
     X = np.random.default_rng(1).standard_normal((M, K)).astype(np.float16)
     got = _matvec(4, X, W, S, N, K, G, "f16").astype(np.float32)
     assert np.abs(got).max() < 1e-4
+
+
+def test_smollm2_layer_shapes_int4_g32():
+    """One SmolLM2-135M layer's seven linears (int4 g32, M = 1) and the LM-head shape."""
+    from locomp_amd import synth as sy
+    for i, (N, K) in enumerate(sy.SMOLLM2_LAYER + [(4096, 576)]):
+        X, W, S = sy.matvec_case(4, 1, N, K, 32, 0.001, 0.01, seed=100 + i)
+        got = _matvec(4, X, W, S, N, K, 32, "f16")
+        _close(got, _oracle(4, X, W, S, 32))
