@@ -60,35 +60,7 @@ __device__ __forceinline__ int b_lds_off(int n, int c) { return n * kBK + ((c ^ 
 // and would drain vmcnt before every LDS read) stays out of the loop; every
 // wait is placed by hand and names the registers it guards, so no consumer
 // can be scheduled before it.  M0 is used by nothing else in this kernel.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-// 16 bytes per lane from global memory to LDS (lane L -> lds + 16 L).
-__device__ __forceinline__ void dma16(const void* g, const void* lds) {
-  const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-  __asm__ volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                   :: "v"(g), "s"(a) : "memory", "m0");
-}
-__device__ __forceinline__ u32x4_t gload_b128(const void* g) {
-  u32x4_t v;
-  __asm__ volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(g) : "memory");
-  return v;
-}
-__device__ __forceinline__ u32x2_t gload_b64(const void* g) {
-  u32x2_t v;
-  __asm__ volatile("global_load_dwordx2 %0, %1, off nt" : "=v"(v) : "v"(g) : "memory");
-  return v;
-}
-__device__ __forceinline__ uint32_t gload_u16(const void* g) {
-  uint32_t v;
-  __asm__ volatile("global_load_ushort %0, %1, off" : "=v"(v) : "v"(g) : "memory");
-  return v;
-}
-__device__ __forceinline__ uint32_t gload_b32(const void* g) {
-  uint32_t v;
-  __asm__ volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(g) : "memory");
-  return v;
-}
+// (lds_addr, dma16 and the gload_* helpers live in lq_common.h.)
 
 // A (activation) tile in LDS: BM rows x 64 k fp16 = 128 B per row, 16-byte
 // chunk c of row m stored at chunk position c ^ (m & 7).
@@ -279,6 +251,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
 
 #undef WAIT_FAR
 #undef FAR_TO_NEAR
+  // The last steps' A copies (clamped repeats) are still in flight: drain
+  // them before the workgroup's LDS can be handed to another workgroup.
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   // Epilogue: lane holds rows 4 * (lane / 16) + r, column lane % 16 of each tile.
 #pragma unroll
   for (int i = 0; i < TM; ++i) {

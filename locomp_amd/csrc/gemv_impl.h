@@ -20,6 +20,7 @@
 // l's A operand is X[m = l % 16, same k].  Scales: post-scale in fp32 when a
 // k-step lies in one group, else the B operand is scaled in fp16.
 #include "lq_common.h"
+#include <type_traits>
 
 namespace lq {
 
@@ -889,6 +890,296 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   }
 }
 
+
+// ------------------------------------------- decode GEMV, 2 <= M <= 16 --
+// A workgroup of 8 waves owns 16 T weight rows (T = 1 .. 4 16-row MFMA tiles,
+// weight row = MFMA column; T is picked so the grid is at most one workgroup
+// per CU) and all M <= 16 activation rows (the MFMA rows).  The weight rows
+// stream through LDS in chunks of 512 bytes per row:
+//   * a chunk (16 T rows, 8 T KB) is copied global -> LDS by direct-to-LDS
+//     loads, 1 KB contiguous per wave instruction (two rows); 16-byte position
+//     p of row r holds logical position p ^ (r & 15), so the 16 rows one LDS
+//     read touches fall in 16 different bank groups;
+//   * a 4-slot ring keeps chunks c + 1 .. c + 3 in flight while chunk c is
+//     consumed, each together with its activations and scales (one "group"
+//     of loads per chunk, issued three chunks ahead: under full load even L2
+//     hits take microseconds); the loads are inline asm and every wait is
+//     placed by hand;
+//   * wave w takes k-eighth w of the chunk (64 bytes per row) for all row
+//     tiles: 4 MFMA blocks per tile, each over one weight dword per lane
+//     (int4: 16x16x32, 32 k; int8: 16x16x16, 16 k), so a group of G >= the
+//     block is applied in fp32 to a chain of whole blocks;
+//   * int4 weights are decoded biased (5 VALU per dword: 1024 + q, or
+//     1024 + 16 q against an activation pre-divided by 16); the bias of a
+//     scale group is one extra MFMA chain per wave (activations x constant),
+//     shared by all tiles, that starts every tile's chain;
+//   * the eight k-eighths are summed through LDS at the end.
+constexpr int kTChunkB = 512;           // bytes per row per chunk
+constexpr int kTSlots = 4;
+constexpr int kTWaves = 8;
+constexpr int kTBlocks = 4;             // MFMA blocks per wave per chunk
+
+template <int WBITS> struct TileMfma;
+template <> struct TileMfma<4> {
+  static constexpr int kSpan = 32;      // k per MFMA block (one dword of int4)
+  static constexpr bool kBiased = true;
+  typedef h8 op_t;
+  typedef u32x4_t x_t;                  // 8 activations per lane per block
+  // (k0, k4) (k1, k5) (k2, k6) (k3, k7) as 1024 + q, 1024 + 16 q, 1024 + q, 1024 + 16 q
+  __device__ static op_t decode(uint32_t w, uint32_t magic) {
+    const uint32_t w8 = w >> 8;
+    u32x4_t b;
+    b.x = and_or(w, 0x000F000Fu, magic);
+    b.y = and_or(w, 0x00F000F0u, magic);
+    b.z = and_or(w8, 0x000F000Fu, magic);
+    b.w = and_or(w8, 0x00F000F0u, magic);
+    return __builtin_bit_cast(h8, b);
+  }
+  // activations in the same order, the 16 q slots divided by 16 (exact)
+  __device__ static op_t prep_x(const x_t& x) {
+    const half2_t sixteenth = {half_t(0.0625f), half_t(0.0625f)};
+    u32x4_t v = xperm8(x);
+    v.y = as_u32(as_h2(v.y) * sixteenth);
+    v.w = as_u32(as_h2(v.w) * sixteenth);
+    return __builtin_bit_cast(h8, v);
+  }
+  // -(bias) per slot: x * (1024 + q) - 1032 x = x (q - 8); (x / 16)(1024 + 16 q) - 1152 (x / 16) = x (q - 8)
+  __device__ static op_t neg_bias() {
+    const half2_t a = {half_t(-1032.f), half_t(-1032.f)};
+    const half2_t b = {half_t(-1152.f), half_t(-1152.f)};
+    u32x4_t v;
+    v.x = as_u32(a); v.y = as_u32(b); v.z = as_u32(a); v.w = as_u32(b);
+    return __builtin_bit_cast(h8, v);
+  }
+  __device__ static float4_t mfma(const op_t& a, const op_t& b, const float4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+template <> struct TileMfma<8> {
+  static constexpr int kSpan = 16;      // k per MFMA block (one dword of int8)
+  static constexpr bool kBiased = false;
+  typedef h4 op_t;
+  typedef u32x2_t x_t;                  // 4 activations per lane per block
+  __device__ static op_t decode(uint32_t w, uint32_t) {
+    half2_t hb[2];
+    int8x4_to_h2(w, hb);
+    h4 r;
+    r[0] = hb[0][0]; r[1] = hb[0][1]; r[2] = hb[1][0]; r[3] = hb[1][1];
+    return r;
+  }
+  __device__ static op_t prep_x(const x_t& x) { return __builtin_bit_cast(h4, x); }
+  __device__ static op_t neg_bias() { return op_t{}; }
+  __device__ static float4_t mfma(const op_t& a, const op_t& b, const float4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kTScaleLds = 32 * 1024;  // LDS for one workgroup's scale rows
+
+// Copies 16 bytes per lane from a raw buffer (offset voff) to LDS (lane L ->
+// lds + 16 L); bytes past the buffer's size read as zero.
+__device__ __forceinline__ void dma16_buf(i32x4_t rsrc, uint32_t voff, const void* lds) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                   :: "v"(voff), "s"(rsrc), "s"(a) : "memory", "m0");
+}
+
+// NSC = scale groups per wave k-eighth of a row (1, 2 or 4; 4 MFMA blocks);
+// TILES = 16-row weight tiles per workgroup (1 .. 4).
+template <int WBITS, int NSC, int TILES, int SD, int OD>
+__global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  typedef TileMfma<WBITS> Mf;
+  typedef typename Mf::op_t op_t;
+  typedef typename Mf::x_t x_t;
+  constexpr int kSpan = Mf::kSpan;                      // k per MFMA block
+  constexpr int kEighthK = kTBlocks * kSpan;            // k per wave per chunk
+  constexpr int kChunkK = kTWaves * kEighthK;
+  constexpr int kPerScale = kTBlocks / NSC;             // blocks sharing one scale
+  constexpr int kSSize = SD == LQ_F32 ? 4 : 2;
+  constexpr int kRows = 16 * TILES;
+  constexpr int kDma = TILES;                           // DMA instructions per wave per chunk
+  constexpr int kSlotB = kRows * kTChunkB;
+  static_assert(kTSlots * kSlotB >= kTWaves * TILES * 64 * 16, "reduction reuses the ring");
+  static_assert(kTSlots * kSlotB + kTScaleLds <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) uint8_t wl[kTSlots * kSlotB];
+  __shared__ __attribute__((aligned(16))) uint8_t sl[kTScaleLds];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int n0 = blockIdx.x * kRows;
+  const int row_bytes = (WBITS == 4) ? (K >> 1) : K;
+  const int nchunks = row_bytes / kTChunkB;
+
+  // DMA: wave w copies rows 2 T w .. 2 T w + 2 T - 1 of each chunk, 2 rows
+  // per instruction.
+  const uint8_t* dsrc[kDma];
+#pragma unroll
+  for (int i = 0; i < kDma; ++i) {
+    const int row = wave * 2 * kDma + 2 * i + (lane >> 5);
+    const int n = min(n0 + row, N - 1);
+    const int c = (lane & 31) ^ (row & 15);
+    dsrc[i] = W + size_t(n) * row_bytes + c * 16;
+  }
+  // Workgroups start at different chunks (step c reads chunk (c + rot) mod
+  // nchunks) so that concurrent workgroups of one XCD read different
+  // activation ranges instead of all hitting the same L2 lines.
+  const int rot = (blockIdx.x >> 3) % nchunks;
+  auto phys = [&](int c) { return c + rot < nchunks ? c + rot : c + rot - nchunks; };
+  auto dma_chunk = [&](int slot, int c) {
+    const int ch = phys(c);
+#pragma unroll
+    for (int i = 0; i < kDma; ++i)
+      dma16(dsrc[i] + ch * kTChunkB, &wl[slot * kSlotB + (wave * 2 * kDma + 2 * i) * kTChunkB]);
+  };
+
+  // Lane (m = r16, q4) supplies activation row m, k = block * kSpan + q4 * kSpan / 4 + 0 ..
+  const half_t* xrow = X + size_t(min(r16, M - 1)) * K + wave * kEighthK + q4 * (kSpan / 4);
+  struct Batch {
+    x_t x[kTBlocks];
+  };
+  auto load_batch = [&](Batch& bt, int c) {
+    const int ch = phys(c);
+#pragma unroll
+    for (int f = 0; f < kTBlocks; ++f) {
+      const half_t* px = xrow + ch * kChunkK + f * kSpan;
+      if constexpr (sizeof(x_t) == 16) {
+        bt.x[f] = gload_b128_cached(px);
+      } else {
+        __asm__ volatile("global_load_dwordx2 %0, %1, off" : "=v"(bt.x[f]) : "v"(px) : "memory");
+      }
+    }
+  };
+  // A group = everything chunk c needs: its activation/scale batch and its
+  // weight DMA.  Name the batch registers after the wait that covers them so
+  // nothing reads them early.
+  constexpr int kGroupLoads = kTBlocks + kDma;
+  auto tie_batch = [&](Batch& bt) {
+#pragma unroll
+    for (int f = 0; f < kTBlocks; ++f) __asm__ volatile("" : "+v"(bt.x[f]));
+  };
+  // Wait until at most `pending` later groups are outstanding (vmcnt takes an
+  // immediate, hence the branches).
+  auto wait_group = [&](Batch& bt, int pending) {
+    if (pending >= 2) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kGroupLoads) : "memory");
+    else if (pending == 1) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(kGroupLoads) : "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    tie_batch(bt);
+  };
+  auto issue_group = [&](Batch& bt, int c) {
+    load_batch(bt, c);
+    dma_chunk(c & 3, c);
+  };
+
+  const uint32_t magic = opaque_u32(0x64006400u);
+  float4_t acc[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int c, const Batch& bt) {
+    const int slot = c & 3;
+    const int kbase = phys(c) * kChunkK + wave * kEighthK;   // first k of this wave's eighth
+    op_t xa[kTBlocks];
+#pragma unroll
+    for (int f = 0; f < kTBlocks; ++f) xa[f] = Mf::prep_x(bt.x[f]);
+    const uint8_t* lslot = &wl[slot * kSlotB];
+#pragma unroll
+    for (int sg = 0; sg < NSC; ++sg) {
+      // bias chain of this scale group: one MFMA per block, shared by the tiles
+      float4_t start = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (Mf::kBiased) {
+        const op_t nb = Mf::neg_bias();
+#pragma unroll
+        for (int fb = 0; fb < kPerScale; ++fb) start = Mf::mfma(xa[sg * kPerScale + fb], nb, start);
+      }
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        const int row = t * 16 + r16;
+        const uint8_t* lrow = lslot + row * kTChunkB + q4 * 4;
+        float4_t part = start;
+#pragma unroll
+        for (int fb = 0; fb < kPerScale; ++fb) {
+          const int f = sg * kPerScale + fb;
+          const int lc = wave * kTBlocks + f;         // 16-byte position of block f
+          const uint32_t w = *reinterpret_cast<const uint32_t*>(lrow + ((lc ^ (row & 15)) << 4));
+          part = Mf::mfma(xa[f], Mf::decode(w, magic), part);
+        }
+        const int g = (kbase + sg * kPerScale * kSpan) / group;
+        const uint8_t* ps = sl + (size_t(row) * num_scales + g) * kSSize;
+        float sc;
+        if constexpr (SD == LQ_F32) sc = *reinterpret_cast<const float*>(ps);
+        else if constexpr (SD == LQ_F16) sc = float(*reinterpret_cast<const half_t*>(ps));
+        else sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
+        acc[t] += part * sc;
+        // Keep this read of the MFMA result in the block of its MFMA chain:
+        // sunk past the step's branches and barrier, it was emitted without
+        // the wait states an MFMA result needs before a VALU read.
+        __asm__ volatile("" : "+v"(acc[t]));
+      }
+    }
+  };
+
+  // Step c issues group c + 3 (into ring slot and register batch (c + 3) % 4,
+  // both released by step c - 1), consumes chunk c, then waits for group
+  // c + 1, leaving groups c + 2 and c + 3 in flight.  Groups are issued in
+  // chunk order and retire in order, so each wait is exact; no load is
+  // issued for a chunk that does not exist.
+  // The workgroup's scale rows n0 .. are contiguous: copy them to LDS first
+  // (the launcher guarantees they fit and are whole 16-byte granules).
+  {
+    const int rows = min(kRows, N - n0);
+    const uint32_t bytes = uint32_t(rows) * uint32_t(num_scales) * kSSize;
+    const uint64_t base = reinterpret_cast<uint64_t>(S) + uint64_t(n0) * num_scales * kSSize;
+    const i32x4_t rsrc = {int(uint32_t(base)), int(uint32_t(base >> 32) & 0xFFFFu), int(bytes),
+                          0x00020000};
+    const int ninstr = int((bytes + 1023) >> 10);
+    for (int j = wave; j < ninstr; j += kTWaves)
+      dma16_buf(rsrc, uint32_t(j * 1024 + lane * 16), &sl[j * 1024]);
+  }
+  Batch bt0, bt1, bt2, bt3;
+  issue_group(bt0, 0);
+  if (nchunks > 1) issue_group(bt1, 1);
+  if (nchunks > 2) issue_group(bt2, 2);
+  wait_group(bt0, min(nchunks - 1, 2));
+  __syncthreads();
+
+  auto step = [&](int c, Batch& cur, Batch& next, Batch& ahead3) {
+    if (c + 3 < nchunks) issue_group(ahead3, c + 3);
+    compute(c, cur);
+    if (c + 1 < nchunks) wait_group(next, min(nchunks - c - 2, 2));
+    __syncthreads();
+  };
+  for (int c = 0; c < nchunks; c += 4) {
+    step(c, bt0, bt1, bt3);
+    if (c + 1 < nchunks) step(c + 1, bt1, bt2, bt0);
+    if (c + 2 < nchunks) step(c + 2, bt2, bt3, bt1);
+    if (c + 3 < nchunks) step(c + 3, bt3, bt0, bt2);
+  }
+
+  // Every load has been waited for and every wave has finished with the
+  // ring (the last step ended in a barrier): reuse it for the cross-wave sum.
+  float4_t* red = reinterpret_cast<float4_t*>(wl);
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) red[(wave * TILES + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  if (wave < TILES) {
+    const int t = wave;
+    float4_t v = red[t * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < kTWaves; ++w) v += red[(w * TILES + t) * 64 + lane];
+    const int n = n0 + t * 16 + r16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = q4 * 4 + r;
+      if (m < M && n < N) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+    }
+  }
+}
+
 template <int WAVES, int KSPLIT>
 static size_t gemv_lds_bytes(int64_t M, int64_t K, int64_t num_scales, int ssize, int step) {
   return size_t(M) * (K + 8) * 2 +
@@ -1033,6 +1324,64 @@ static bool gemv_seg_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G) {
          M * K * 2 < (int64_t(1) << 31) && N * (K / G) * 4 < (int64_t(1) << 31);
 }
 
+// Tiles per workgroup for the LDS-ring kernel: the smallest count whose grid
+// fits one workgroup per CU (256 CUs, so no CU streams the activations
+// twice), else 4; then fewer while the workgroup's scale rows exceed their
+// LDS area.  0 = the scale rows of even one tile do not fit.
+static int gemv_tile_count(int64_t N, int64_t K, int64_t G, int scale_bytes) {
+  int tiles = 4;
+  for (int t = 1; t <= 4; ++t)
+    if ((N + 16 * t - 1) / (16 * t) <= 256) { tiles = t; break; }
+  const int64_t row_scale_bytes = (K / G) * scale_bytes;
+  while (tiles > 0 && 16 * tiles * row_scale_bytes > kTScaleLds) --tiles;
+  return tiles;
+}
+
+template <int WBITS, int NSC, int SD, int OD>
+static void launch_gemv_tile_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                               int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int tiles = gemv_tile_count(N, K, G, SD == LQ_F32 ? 4 : 2);
+  const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
+#define LQ_TILE_LAUNCH(T_)                                                                     \
+  hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, SD, OD>), dim3(blocks), dim3(512), 0,   \
+                     st, static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,  \
+                     int(M), int(N), int(K), int(K / G), int(G))
+  switch (tiles) {
+    case 1: LQ_TILE_LAUNCH(1); break;
+    case 2: LQ_TILE_LAUNCH(2); break;
+    case 3: LQ_TILE_LAUNCH(3); break;
+    default: LQ_TILE_LAUNCH(4); break;
+  }
+#undef LQ_TILE_LAUNCH
+}
+
+template <int WBITS, int SD, int OD>
+static int launch_gemv_tile(const void* X, const void* W, const void* S, void* O, int64_t M,
+                            int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int64_t eighth_k = kTBlocks * TileMfma<WBITS>::kSpan;
+  const int nsc = G >= eighth_k ? 1 : int(eighth_k / G);
+  switch (nsc) {
+    case 1: launch_gemv_tile_t<WBITS, 1, SD, OD>(X, W, S, O, M, N, K, G, st); break;
+    case 2: launch_gemv_tile_t<WBITS, 2, SD, OD>(X, W, S, O, M, N, K, G, st); break;
+    default: launch_gemv_tile_t<WBITS, 4, SD, OD>(X, W, S, O, M, N, K, G, st); break;
+  }
+  return check_launch();
+}
+
+// The LDS-ring tile kernel: 2 <= M <= 16, whole 512-byte chunks per row,
+// every wave k-eighth (128 k int4 / 64 k int8) either inside one group or
+// split into 2 or 4 whole groups of at least one MFMA block, and each row's
+// scales a whole number of 16-byte granules that fit the LDS scale area.
+static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, int scale_bytes) {
+  const int64_t row_bytes = wbits == 4 ? K / 2 : K;
+  const int64_t span = wbits == 4 ? 32 : 16;
+  const int64_t eighth_k = kTBlocks * span;
+  const bool groups_ok = G >= eighth_k ? G % eighth_k == 0
+                                       : (G >= span && eighth_k % G == 0);
+  return M >= 1 && M <= 16 && row_bytes >= kTChunkB && row_bytes % kTChunkB == 0 && groups_ok &&
+         ((K / G) * scale_bytes) % 16 == 0 && gemv_tile_count(N, K, G, scale_bytes) > 0;
+}
+
 // The diagonal-MFMA kernel applies to int4, M <= 4, G % 128 == 0, K <= 16384.
 static bool gemv_diag_ok(int wbits, int64_t M, int64_t K, int64_t G) {
   return wbits == 4 && M <= 4 && G % 128 == 0 && K % 128 == 0 && K <= 16384 && K >= 128;
@@ -1055,6 +1404,10 @@ static int launch_skinny_mt(const void* X, const void* W, const void* S, void* O
 template <int WBITS, int SD, int OD>
 static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void* O, int64_t M,
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
+    if (M >= 2 && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
+      return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
+  }
   if constexpr (WBITS == 4 && SD != LQ_BF16 && OD != LQ_BF16) {
     if (gemv_seg_ok(WBITS, M, N, K, G)) {
       if (M == 1) return launch_gemv_seg_m<1, SD, OD>(X, W, S, O, M, N, K, G, st);

@@ -17,6 +17,7 @@ namespace lq {
 typedef _Float16 half_t;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -168,6 +169,59 @@ __device__ __forceinline__ u32x4_t xperm8(u32x4_t d) {
 __host__ __forceinline__ int check_launch() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LQ_OK : int(e);
+}
+
+// ------------------------------------------------------ explicit loads --
+// Global loads issued with inline asm, for kernels that place every vmcnt
+// wait by hand (the compiler does not count asm loads, and it treats an
+// LDS-DMA as a write to all of LDS).  A register written by one of these
+// must not be read before an asm wait that names it.  dma16 uses M0.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// 16 bytes per lane from global memory to LDS (lane L -> lds + 16 L).
+__device__ __forceinline__ void dma16(const void* g, const void* lds) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  __asm__ volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                   :: "v"(g), "s"(a) : "memory", "m0");
+}
+__device__ __forceinline__ u32x4_t gload_b128(const void* g) {
+  u32x4_t v;
+  __asm__ volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+__device__ __forceinline__ u32x2_t gload_b64(const void* g) {
+  u32x2_t v;
+  __asm__ volatile("global_load_dwordx2 %0, %1, off nt" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t gload_u16(const void* g) {
+  uint32_t v;
+  __asm__ volatile("global_load_ushort %0, %1, off" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t gload_b32(const void* g) {
+  uint32_t v;
+  __asm__ volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+
+__device__ __forceinline__ u32x4_t gload_b128_cached(const void* g) {
+  u32x4_t v;
+  __asm__ volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+// Raw bits of scale i (fp32 word or 16-bit pattern) and their value.
+template <int DT>
+__device__ __forceinline__ uint32_t gload_scale_bits(const void* p, size_t i) {
+  if constexpr (DT == LQ_F32) return gload_b32(static_cast<const float*>(p) + i);
+  else return gload_u16(static_cast<const uint16_t*>(p) + i);
+}
+template <int DT>
+__device__ __forceinline__ float scale_from_bits(uint32_t b) {
+  if constexpr (DT == LQ_F32) return __builtin_bit_cast(float, b);
+  else if constexpr (DT == LQ_F16) return float(__builtin_bit_cast(half_t, uint16_t(b)));
+  else return __builtin_bit_cast(float, b << 16);
 }
 
 }  // namespace lq

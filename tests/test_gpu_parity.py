@@ -143,6 +143,20 @@ def test_matvec_fp16_small(policy, wbits, M, N, K, G):
     _close(got, _oracle(wbits, X, W, S, G))
 
 
+@pytest.mark.parametrize("wbits", [4, 8])
+@pytest.mark.parametrize("M,N,K,G", [
+    (2, 37, 1024, 32), (3, 1000, 2048, 128), (8, 64, 6144, 64), (16, 33, 3072, 1024),
+    (5, 250, 4096, 16), (16, 11008, 1024, 128), (12, 96, 2560, 512), (9, 13000, 1024, 64)])
+def test_matvec_lds_ring_shapes(wbits, M, N, K, G):
+    """Decode sizes 2 <= M <= 16 with whole 512-byte row chunks (the LDS-ring
+    kernel): ragged N, odd chunk counts, post-scaled and pre-scaled groups."""
+    if wbits == 4 and G % 32:
+        pytest.skip("int4 groups hold whole 32-k lane spans")
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=7 * M + N + K)
+    got = _matvec(wbits, X, W, S, N, K, G, "f16")
+    _close(got, _oracle(wbits, X, W, S, G))
+
+
 @pytest.mark.parametrize("M,N,K,G", [(96, 160, 256, 128), (130, 64, 512, 32), (256, 256, 1024, 64)])
 def test_matmul_prefill_small(policy, M, N, K, G):
     X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K)
