@@ -1043,8 +1043,13 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   struct Batch {
     x_t x[kTBlocks];
   };
+  // Lanes of activation rows m >= M load nothing (their registers hold
+  // whatever they held): MFMA rows are independent and rows m >= M are never
+  // stored, so this only saves requests.
+  const bool x_lane = r16 < M;
   auto load_batch = [&](Batch& bt, int c) {
     const int ch = phys(c);
+    if (!x_lane) return;
 #pragma unroll
     for (int f = 0; f < kTBlocks; ++f) {
       const half_t* px = xrow + ch * kChunkK + f * kSpan;
@@ -1083,10 +1088,33 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   auto compute = [&](int c, const Batch& bt) {
     const int slot = c & 3;
     const int kbase = phys(c) * kChunkK + wave * kEighthK;   // first k of this wave's eighth
+    const uint8_t* lslot = &wl[slot * kSlotB];
+    // All LDS reads first (weights: one dword per tile and block; scales),
+    // so their latency overlaps; then the tile chains interleaved block by
+    // block so consecutive MFMAs are independent.
+    uint32_t w[TILES][kTBlocks];
+    float sc[TILES][NSC];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const int row = t * 16 + r16;
+      const uint8_t* lrow = lslot + row * kTChunkB + q4 * 4;
+#pragma unroll
+      for (int f = 0; f < kTBlocks; ++f) {
+        const int lc = wave * kTBlocks + f;           // 16-byte position of block f
+        w[t][f] = *reinterpret_cast<const uint32_t*>(lrow + ((lc ^ (row & 15)) << 4));
+      }
+#pragma unroll
+      for (int sg = 0; sg < NSC; ++sg) {
+        const int g = (kbase + sg * kPerScale * kSpan) / group;
+        const uint8_t* ps = sl + (size_t(row) * num_scales + g) * kSSize;
+        if constexpr (SD == LQ_F32) sc[t][sg] = *reinterpret_cast<const float*>(ps);
+        else if constexpr (SD == LQ_F16) sc[t][sg] = float(*reinterpret_cast<const half_t*>(ps));
+        else sc[t][sg] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
+      }
+    }
     op_t xa[kTBlocks];
 #pragma unroll
     for (int f = 0; f < kTBlocks; ++f) xa[f] = Mf::prep_x(bt.x[f]);
-    const uint8_t* lslot = &wl[slot * kSlotB];
 #pragma unroll
     for (int sg = 0; sg < NSC; ++sg) {
       // bias chain of this scale group: one MFMA per block, shared by the tiles
@@ -1096,25 +1124,18 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
 #pragma unroll
         for (int fb = 0; fb < kPerScale; ++fb) start = Mf::mfma(xa[sg * kPerScale + fb], nb, start);
       }
+      float4_t part[TILES];
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) part[t] = start;
+#pragma unroll
+      for (int fb = 0; fb < kPerScale; ++fb) {
+        const int f = sg * kPerScale + fb;
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) part[t] = Mf::mfma(xa[f], Mf::decode(w[t][f], magic), part[t]);
+      }
 #pragma unroll
       for (int t = 0; t < TILES; ++t) {
-        const int row = t * 16 + r16;
-        const uint8_t* lrow = lslot + row * kTChunkB + q4 * 4;
-        float4_t part = start;
-#pragma unroll
-        for (int fb = 0; fb < kPerScale; ++fb) {
-          const int f = sg * kPerScale + fb;
-          const int lc = wave * kTBlocks + f;         // 16-byte position of block f
-          const uint32_t w = *reinterpret_cast<const uint32_t*>(lrow + ((lc ^ (row & 15)) << 4));
-          part = Mf::mfma(xa[f], Mf::decode(w, magic), part);
-        }
-        const int g = (kbase + sg * kPerScale * kSpan) / group;
-        const uint8_t* ps = sl + (size_t(row) * num_scales + g) * kSSize;
-        float sc;
-        if constexpr (SD == LQ_F32) sc = *reinterpret_cast<const float*>(ps);
-        else if constexpr (SD == LQ_F16) sc = float(*reinterpret_cast<const half_t*>(ps));
-        else sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
-        acc[t] += part * sc;
+        acc[t] += part[t] * sc[t][sg];
         // Keep this read of the MFMA result in the block of its MFMA chain:
         // sunk past the step's branches and barrier, it was emitted without
         // the wait states an MFMA result needs before a VALU read.
