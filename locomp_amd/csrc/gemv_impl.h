@@ -1149,13 +1149,16 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   // c + 1, leaving groups c + 2 and c + 3 in flight.  Groups are issued in
   // chunk order and retire in order, so each wait is exact; no load is
   // issued for a chunk that does not exist.
-  // The workgroup's scale rows n0 .. are contiguous: copy them to LDS first
-  // (the launcher guarantees they fit and are whole 16-byte granules).
+  // The workgroup's scale rows n0 .. are contiguous: copy them to LDS first.
+  // The buffer runs to the end of the scale array (a whole number of dwords,
+  // checked by the launcher), so every wanted byte sits in an in-range dword
+  // and whatever lies past the array reads as zero.
   {
     const int rows = min(kRows, N - n0);
     const uint32_t bytes = uint32_t(rows) * uint32_t(num_scales) * kSSize;
+    const uint32_t avail = uint32_t(N - n0) * uint32_t(num_scales) * kSSize;
     const uint64_t base = reinterpret_cast<uint64_t>(S) + uint64_t(n0) * num_scales * kSSize;
-    const i32x4_t rsrc = {int(uint32_t(base)), int(uint32_t(base >> 32) & 0xFFFFu), int(bytes),
+    const i32x4_t rsrc = {int(uint32_t(base)), int(uint32_t(base >> 32) & 0xFFFFu), int(avail),
                           0x00020000};
     const int ninstr = int((bytes + 1023) >> 10);
     for (int j = wave; j < ninstr; j += kTWaves)
@@ -1391,8 +1394,8 @@ static int launch_gemv_tile(const void* X, const void* W, const void* S, void* O
 
 // The LDS-ring tile kernel: 2 <= M <= 16, whole 512-byte chunks per row,
 // every wave k-eighth (128 k int4 / 64 k int8) either inside one group or
-// split into 2 or 4 whole groups of at least one MFMA block, and each row's
-// scales a whole number of 16-byte granules that fit the LDS scale area.
+// split into 2 or 4 whole groups of at least one MFMA block, and the scale
+// array a whole number of dwords whose rows fit the LDS scale area.
 static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, int scale_bytes) {
   const int64_t row_bytes = wbits == 4 ? K / 2 : K;
   const int64_t span = wbits == 4 ? 32 : 16;
@@ -1400,7 +1403,7 @@ static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, 
   const bool groups_ok = G >= eighth_k ? G % eighth_k == 0
                                        : (G >= span && eighth_k % G == 0);
   return M >= 1 && M <= 16 && row_bytes >= kTChunkB && row_bytes % kTChunkB == 0 && groups_ok &&
-         ((K / G) * scale_bytes) % 16 == 0 && gemv_tile_count(N, K, G, scale_bytes) > 0;
+         (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_count(N, K, G, scale_bytes) > 0;
 }
 
 // The diagonal-MFMA kernel applies to int4, M <= 4, G % 128 == 0, K <= 16384.

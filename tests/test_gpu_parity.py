@@ -157,6 +157,20 @@ def test_matvec_lds_ring_shapes(wbits, M, N, K, G):
     _close(got, _oracle(wbits, X, W, S, G))
 
 
+@pytest.mark.parametrize("wbits", [4, 8])
+@pytest.mark.parametrize("M,N,K,G", [
+    (17, 64, 1024, 64), (33, 300, 2048, 16), (64, 1000, 4096, 4096), (48, 4100, 1536, 512),
+    (16, 1000, 4096, 4096), (3, 77, 1024, 1024)])
+def test_matvec_many_rows_and_per_channel(wbits, M, N, K, G):
+    """Decode/verify sizes up to M = 64 and per-channel / large groups
+    (one or few scales per row, whose scale rows are not 16-byte multiples)."""
+    if wbits == 4 and G % 32:
+        pytest.skip("int4 groups hold whole 32-k lane spans")
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=3 * M + N + K)
+    got = _matvec(wbits, X, W, S, N, K, G, "f16")
+    _close(got, _oracle(wbits, X, W, S, G))
+
+
 @pytest.mark.parametrize("M,N,K,G", [(96, 160, 256, 128), (130, 64, 512, 32), (256, 256, 1024, 64)])
 def test_matmul_prefill_small(policy, M, N, K, G):
     X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K)
