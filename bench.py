@@ -107,6 +107,33 @@ class Case:
         return self.O[0].cpu().numpy()
 
 
+class QuantCase:
+    """GPU weight producer (quantize_int4 of examples/38:248-271): float32
+    weights [N, K] -> packed int4 + float32 scales, weight replicas rotated."""
+
+    def __init__(self, N, K, G, seed=0, min_bytes=LLC_BYTES * 5 // 4):
+        import torch
+        from locomp_amd import _lib
+        self.N, self.K, self.G = N, K, G
+        rng = np.random.default_rng(seed)
+        w0 = _dev(rng.standard_normal((N, K), dtype=np.float32))
+        self.R = max(1, math.ceil(min_bytes / w0.numel() / 4))
+        self.W = [w0] + [w0.clone() for _ in range(self.R - 1)]
+        self.Q = torch.empty(N * K // 2, dtype=torch.uint8, device="cuda")
+        self.S = torch.empty(N * (K // G), dtype=torch.float32, device="cuda")
+        self.algo_bytes = N * K * 4 + N * K // 2 + N * (K // G) * 4
+        self.flops = 0
+        self.lib = _lib.load()
+        torch.cuda.synchronize()
+
+    def launch(self, i, stream):
+        vp = ctypes.c_void_p
+        rc = self.lib.locomp_amd_quantize_int4(vp(self.W[i % self.R].data_ptr()), vp(self.Q.data_ptr()),
+                                               vp(self.S.data_ptr()), self.N, self.K, self.G, 0, 0, stream)
+        if rc != 0:
+            raise RuntimeError(f"launch failed: {rc}")
+
+
 class Stack:
     """SmolLM2-135M-shaped decode linear stack: 30 layers x 7 int4 g32 GEMVs
     (q, k, v, o, gate, up, down) at M = 1, random weights (BASELINE config 5b).
@@ -316,6 +343,8 @@ def main():
         c = synth.CFG2
         run_case("dequant_int4_4096x4096_g32_f16",
                  Case("dequant", 4, 0, c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm")
+    if want("quantize"):
+        run_case("quantize_int4_4096x4096_g32_from_f32", QuantCase(4096, 4096, 32), "hbm")
     if want("smollm2"):
         for fused in (False, True):
             st = Stack(fused=fused)

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define LOCOMP_AMD_ABI_VERSION 1
+#define LOCOMP_AMD_ABI_VERSION 2
 
 /* Element dtype codes. */
 enum {
@@ -57,6 +57,12 @@ enum {
   LQ_ERR_DTYPE = -2,   /* unknown dtype code                          */
   LQ_ERR_NULL = -3,    /* null pointer with a non-empty problem        */
   LQ_ERR_POLICY = -4   /* unknown kernel policy                        */
+};
+
+/* Quantizer variants (locomp_amd_quantize_int4). */
+enum {
+  LQ_QUANT_EX38 = 0,  /* quantize_int4, examples/38_quantized_matmul.py:248-271 */
+  LQ_QUANT_EX52 = 1   /* quantize_int4_ref, examples/52_dequantize.py:110-126 */
 };
 
 /* Kernel policies (locomp_amd_set_policy). */
@@ -121,6 +127,25 @@ int locomp_amd_dequant_matvec_int8(const void* X, const void* W,
                                    int64_t GROUP_SIZE, int64_t N, int64_t M,
                                    int x_dtype, int scale_dtype,
                                    int out_dtype, void* stream);
+
+/* Quantize float weights W [N, K] (in_dtype fp32 / fp16 / bf16) on the GPU
+ * into PACKED uint8 [N, K/2] (byte j = q[2j] | q[2j+1] << 4) and float32
+ * SCALES [N, K/GROUP_SIZE], bit-exact with the reference's NumPy producers:
+ *   variant LQ_QUANT_EX38: quantize_int4, examples/38_quantized_matmul.py:248-271
+ *     s = amax > 0 ? amax / 7 : 1;  q = clip(round(w / s) + 8, 0, 15)
+ *   variant LQ_QUANT_EX52: quantize_int4_ref, examples/52_dequantize.py:110-126
+ *     s = max(amax, 1e-10) / 7;     q = clip(round(w / (s + 1e-10)) + 8, 0, 15)
+ * (float32 arithmetic, round half to even).  GROUP_SIZE must divide K and be
+ * even.  The reference runs these on the host as weight producers; here they
+ * are one HBM-bound launch. */
+int locomp_amd_quantize_int4(const void* W, void* PACKED, float* SCALES, int64_t N, int64_t K,
+                             int64_t GROUP_SIZE, int variant, int in_dtype, void* stream);
+
+/* Quantize to int8 Q [N, K] and float32 SCALES [N, K/GROUP_SIZE], bit-exact
+ * with quantize_int8, examples/38_quantized_matmul.py:274-291:
+ *   s = amax > 0 ? amax / 127 : 1;  q = clip(round(w / s), -128, 127). */
+int locomp_amd_quantize_int8(const void* W, void* Q, float* SCALES, int64_t N, int64_t K,
+                             int64_t GROUP_SIZE, int in_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -2,7 +2,8 @@
 
 Drop-in surface for locomp's quantized examples (38, 52, 58): device tensors
 (``tensor / empty / zeros / ones``), dtype markers, the four kernel objects
-with ``kernel[(N,), (128,)](...)`` launches and the ``gpu_*`` wrappers.
+with ``kernel[(N,), (128,)](...)`` launches, the ``gpu_*`` wrappers and the
+GPU weight producers ``quantize_int4 / quantize_int4_ref / quantize_int8``.
 Kernels are hand-written HIP for gfx950 in ``_liblocomp_amd.so`` (built by
 ``python -m locomp_amd.build``), called through its C ABI.
 """
@@ -13,6 +14,7 @@ from .tensor import Tensor, bfloat16, empty, ones, tensor, zeros
 from .kernels import (dequant_int4, dequant_int8, dequant_matmul_int4, dequant_matmul_int8,
                       dequant_matvec_int4, dequant_matvec_int8, quant_matvec_int8)
 from .ops import gpu_dequant_int4, gpu_dequant_int8, gpu_matvec_int4, gpu_matvec_int8
+from .quantize import quantize_int4, quantize_int4_ref, quantize_int8
 from ._lib import LocompAMDError, get_policy, set_policy
 
 __version__ = "0.1.0"
@@ -41,6 +43,7 @@ __all__ = [
     "dequant_int4", "dequant_int8", "dequant_matvec_int4", "dequant_matvec_int8",
     "dequant_matmul_int4", "dequant_matmul_int8", "quant_matvec_int8",
     "gpu_matvec_int4", "gpu_matvec_int8", "gpu_dequant_int4", "gpu_dequant_int8",
+    "quantize_int4", "quantize_int4_ref", "quantize_int8",
     "LocompAMDError", "set_policy", "get_policy",
     "Float16", "UInt8", "Int8", "Int32", "BFloat16", "constexpr",
 ]

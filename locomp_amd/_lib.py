@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_liblocomp_amd.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # dtype codes (LQ_F32 / LQ_F16 / LQ_BF16)
 F32, F16, BF16 = 0, 1, 2
@@ -21,6 +21,8 @@ F32, F16, BF16 = 0, 1, 2
 OK, ERR_SHAPE, ERR_DTYPE, ERR_NULL, ERR_POLICY = 0, -1, -2, -3, -4
 # kernel policies
 POLICY_AUTO, POLICY_GENERIC = 0, 1
+# quantizer variants (LQ_QUANT_EX38 / LQ_QUANT_EX52)
+QUANT_EX38, QUANT_EX52 = 0, 1
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -38,6 +40,8 @@ SIGNATURES = {
                                        _int, _int, _int, _vp],
     "locomp_amd_dequant_matvec_int8": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                        _int, _int, _int, _vp],
+    "locomp_amd_quantize_int4": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp],
+    "locomp_amd_quantize_int8": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
 }
 
 _lib = None

@@ -16,7 +16,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJDIR = PKG / "_build"
 LIB = PKG / "_liblocomp_amd.so"
-SOURCES = ["dequant.hip", "gemv_w4.hip", "gemv_w8.hip", "gemv_generic.hip", "gemm.hip", "capi.hip"]
+SOURCES = ["dequant.hip", "gemv_w4.hip", "gemv_w8.hip", "gemv_generic.hip", "gemm.hip", "quantize.hip",
+           "capi.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -19,6 +19,8 @@ template <int WBITS>
 int launch_gemm(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
                 int, int, hipStream_t);
 int launch_zero_fill(void*, int64_t, int, hipStream_t);
+int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
+                    hipStream_t);
 
 static std::atomic<int> g_policy{LQ_POLICY_AUTO};
 
@@ -147,6 +149,34 @@ int locomp_amd_dequant_matvec_int8(const void* X, const void* W, const void* sca
   if (rc) return rc;
   return matmul_dispatch<8>(X, W, scales, O, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
                             out_dtype, static_cast<hipStream_t>(stream));
+}
+
+// Quantizers.  mode: 0 = examples/38 quantize_int4, 1 = examples/52
+// quantize_int4_ref, 2 = examples/38 quantize_int8.
+static int quantize_common(int mode, const void* W, void* Q, float* S, int64_t N, int64_t K,
+                           int64_t G, int in_dtype, void* stream) {
+  if (!dtype_ok(in_dtype)) return LQ_ERR_DTYPE;
+  if (N < 0 || K < 0 || G <= 0 || K % G != 0) return LQ_ERR_SHAPE;
+  if (mode != 2 && G % 2 != 0) return LQ_ERR_SHAPE;   // int4 packs pairs inside a group
+  if (N == 0 || K == 0) return LQ_OK;
+  if (!W || !Q || !S) return LQ_ERR_NULL;
+  if (N * K > kMax32 * 4) return LQ_ERR_SHAPE;
+  const bool vec_ok = fast_allowed() && K % 8 == 0 && aligned(W, 16) &&
+                      aligned(Q, mode == 2 ? 8 : 4);
+  return launch_quantize(mode, W, Q, S, N, K, G, in_dtype, vec_ok,
+                         static_cast<hipStream_t>(stream));
+}
+
+int locomp_amd_quantize_int4(const void* W, void* PACKED, float* SCALES, int64_t N, int64_t K,
+                             int64_t GROUP_SIZE, int variant, int in_dtype, void* stream) {
+  if (variant != LQ_QUANT_EX38 && variant != LQ_QUANT_EX52) return LQ_ERR_SHAPE;
+  return quantize_common(variant == LQ_QUANT_EX38 ? 0 : 1, W, PACKED, SCALES, N, K, GROUP_SIZE,
+                         in_dtype, stream);
+}
+
+int locomp_amd_quantize_int8(const void* W, void* Q, float* SCALES, int64_t N, int64_t K,
+                             int64_t GROUP_SIZE, int in_dtype, void* stream) {
+  return quantize_common(2, W, Q, SCALES, N, K, GROUP_SIZE, in_dtype, stream);
 }
 
 }  // extern "C"

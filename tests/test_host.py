@@ -69,6 +69,24 @@ def test_c_abi_rejects_bad_shapes_without_launch():
     assert lib.locomp_amd_dequant_matvec_int4(NULL, NULL, NULL, NULL, 64, 32, 2, 32, 4, 0, 1, 1, 1, NULL) == 0
 
 
+def test_quantize_abi_validates_without_a_gpu():
+    lib = _lib.load()
+    q4, q8 = lib.locomp_amd_quantize_int4, lib.locomp_amd_quantize_int8
+    EX38, EX52 = _lib.QUANT_EX38, _lib.QUANT_EX52
+    # (W, PACKED, SCALES, N, K, GROUP_SIZE, variant, in_dtype, stream)
+    assert q4(P, P, P, 4, 64, 24, EX38, 0, NULL) == _lib.ERR_SHAPE     # G does not divide K
+    assert q4(P, P, P, 4, 45, 9, EX38, 0, NULL) == _lib.ERR_SHAPE      # odd int4 group
+    assert q4(P, P, P, 4, 64, 0, EX38, 0, NULL) == _lib.ERR_SHAPE
+    assert q4(P, P, P, -1, 64, 32, EX38, 0, NULL) == _lib.ERR_SHAPE
+    assert q4(P, P, P, 4, 64, 32, 7, 0, NULL) == _lib.ERR_SHAPE        # unknown variant
+    assert q4(P, P, P, 4, 64, 32, EX52, 5, NULL) == _lib.ERR_DTYPE
+    assert q4(NULL, P, P, 4, 64, 32, EX38, 0, NULL) == _lib.ERR_NULL
+    assert q4(NULL, NULL, NULL, 0, 64, 32, EX38, 0, NULL) == 0          # empty: nothing touched
+    assert q8(P, P, P, 4, 64, 24, 0, NULL) == _lib.ERR_SHAPE
+    assert q8(P, NULL, P, 4, 64, 32, 0, NULL) == _lib.ERR_NULL
+    assert q8(P, P, P, 4, 64, 32, 3, NULL) == _lib.ERR_DTYPE
+
+
 def test_check_maps_codes_to_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.ERR_SHAPE, "x")
