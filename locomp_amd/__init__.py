@@ -15,6 +15,7 @@ from .kernels import (dequant_int4, dequant_int8, dequant_matmul_int4, dequant_m
                       dequant_matvec_int4, dequant_matvec_int8, quant_matvec_int8)
 from .ops import gpu_dequant_int4, gpu_dequant_int8, gpu_matvec_int4, gpu_matvec_int8
 from .quantize import quantize_int4, quantize_int4_ref, quantize_int8
+from .checkpoint import QuantizedLinear, load_packed, quantize_checkpoint, read_packed, save_packed
 from ._lib import LocompAMDError, get_policy, set_policy
 
 __version__ = "0.1.0"
@@ -44,6 +45,7 @@ __all__ = [
     "dequant_matmul_int4", "dequant_matmul_int8", "quant_matvec_int8",
     "gpu_matvec_int4", "gpu_matvec_int8", "gpu_dequant_int4", "gpu_dequant_int8",
     "quantize_int4", "quantize_int4_ref", "quantize_int8",
+    "QuantizedLinear", "quantize_checkpoint", "save_packed", "read_packed", "load_packed",
     "LocompAMDError", "set_policy", "get_policy",
     "Float16", "UInt8", "Int8", "Int32", "BFloat16", "constexpr",
 ]
