@@ -1,9 +1,10 @@
 // Prefill-shaped dequant-matmul for gfx950: O[M, N] = X[M, K] @ deq(W)^T with
-// fp16 activations, int4 group-wise weights, fp16 MFMA and fp32 accumulation.
+// fp16 activations, int4 or int8 group-wise weights, fp16 MFMA and fp32
+// accumulation.
 //
 // The reference has no GEMM for this path; it would run one matvec launch per
 // activation row (locomp examples/38_quantized_matmul.py:154).  Values follow
-// the same definition: w = (q - 8) * s[n, k / G].
+// the same definition: w = (q - 8) * s[n, k / G] (int4), q * s (int8).
 //
 // Tiling (default GemmCfg<8, 1, 2, 8>: 512 lanes, BM x BN = 256 x 128, BK = 64):
 //   * Wave w owns output rows [32 w, 32 w + 32) and all 128 columns: 2 x 8
@@ -12,9 +13,9 @@
 //     the gfx950 direct-to-LDS load (global_load_lds_dwordx4): no VGPRs, 128 B
 //     of one row per 8 lanes, XOR-swizzled chunk order chosen through the
 //     source addresses.  A 3-slot ring keeps steps ks + 1 and ks + 2 in flight.
-//   * Weights: the packed 128 x 32-byte tile of step ks + 2 is loaded into
-//     registers during step ks, dequantised during step ks + 1 to exact fp16
-//     (q - 8) times the fp16 scale (one rounding) and written to an
+//   * Weights: the 128 x 32-byte (int4) or 128 x 64-byte (int8) tile of step
+//     ks + 2 is loaded into registers during step ks, dequantised during step
+//     ks + 1 to exact fp16 (q - 8) or q times the fp16 scale (one rounding) and written to an
 //     XOR-swizzled LDS tile (2 stages) that every wave reads as the B operand.
 //   * One barrier per step.  The loop's loads are inline asm with hand-placed
 //     s_waitcnt (the compiler would drain vmcnt before every LDS read after an
@@ -45,9 +46,17 @@ struct GemmCfg {
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int BM = WM * TM * 16;
   static constexpr int BN = WN * TN * 16;
-  // packed weight bytes per step: BN rows x 32 bytes; bytes per loader thread
-  static constexpr int kBBytes = BN * 32 / kThreads;
-  static_assert(kBBytes == 4 || kBBytes == 8 || kBBytes == 16, "B loader granularity");
+};
+
+// Weight bytes of one k-step row (64 k): 32 (int4) or 64 (int8); bytes per
+// loader thread; k covered by one loader thread.
+template <class C, int WBITS>
+struct GemmB {
+  static constexpr int kRowBytes = 64 * WBITS / 8;
+  static constexpr int kBytes = C::BN * kRowBytes / C::kThreads;
+  static constexpr int kPerRow = kRowBytes / kBytes;
+  static constexpr int kSpanK = kBytes * 8 / WBITS;
+  static_assert(kBytes == 8 || kBytes == 16, "64- or 128-bit weight loads");
 };
 
 // LDS element offset (halves) of 16-byte chunk c (of 8 per row) of weight
@@ -67,9 +76,10 @@ __device__ __forceinline__ int b_lds_off(int n, int c) { return n * kBK + ((c ^ 
 __device__ __forceinline__ int a_lds_off(int m, int c) { return m * kBK + ((c ^ (m & 7)) << 3); }
 
 constexpr int kAStages = 3;   // activation ring: steps ks, ks + 1, ks + 2
+constexpr int kGemmScaleFloats = 8192;   // int8 post-scale: BN x (K / G) fp32 scales
 constexpr int kBStages = 2;
 
-template <class C, int SD, int OD>
+template <class C, int WBITS, int SD, int OD>
 __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int tiles_m, int tiles_n) {
@@ -78,6 +88,11 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
   typedef typename Elem<SD>::T stype;
   __shared__ __attribute__((aligned(16))) half_t As[kAStages][BM * kBK];
   __shared__ __attribute__((aligned(16))) half_t Bs[kBStages][BN * kBK];
+  // int8: B holds the exact integers q and the group scales are applied to
+  // fp32 partial sums (a pre-scaled fp16 weight would round |q s| up to 2.5
+  // to 11 bits, too coarse at K = 4096); the tile's scale rows live here.
+  constexpr bool kPost = WBITS == 8;
+  __shared__ float Ssh[kPost ? kGemmScaleFloats : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -94,7 +109,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
   if (total % 8 == 0) t = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
   const int m0 = (t / tiles_n) * BM;
   const int n0 = (t % tiles_n) * BN;
-  const int half_k = K >> 1;
+  const int row_bytes = WBITS == 4 ? (K >> 1) : K;
   const int wrow0 = wm * TM * 16;              // first tile row this wave multiplies
 
   // A DMA: wave w copies rows [w * kDmaRows, (w + 1) * kDmaRows) of the tile
@@ -118,28 +133,31 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
       dma16(adma_src[i] + k0, &As[stage][(drow0 + 8 * i) * kBK]);
   };
 
-  // B loader: C::kBBytes packed bytes (2 k per byte) of one weight row
-  constexpr int kPerRow = 32 / C::kBBytes;
+  // B loader: Bg::kBytes weight bytes (Bg::kSpanK k) of one weight row
+  typedef GemmB<C, WBITS> Bg;
+  constexpr int kPerRow = Bg::kPerRow;
   const int b_n = tid / kPerRow;
   const int b_part = tid % kPerRow;
   const int bn = min(n0 + b_n, N - 1);
-  const uint8_t* wrow = W + size_t(bn) * half_k + b_part * C::kBBytes;
+  const uint8_t* wrow = W + size_t(bn) * row_bytes + b_part * Bg::kBytes;
   const stype* sp = static_cast<const stype*>(S) + size_t(bn) * num_scales;
-  static_assert(C::kBBytes == 16 || C::kBBytes == 8, "64- or 128-bit weight loads");
-  constexpr int kBWords = C::kBBytes / 4;
+  constexpr int kBWords = Bg::kBytes / 4;
   // Packed weights: `bfar` receives the loads of step ks + 2 during step ks;
   // at the end of the step (after its wait) they move to `bnear`, which the
   // next step dequantises while its MFMAs run.
   u32x4_t bfar, bnear;    // 16-byte loads (bnear also holds the 8-byte case)
   u32x2_t bfar2;          // 8-byte loads
-  uint32_t sfar, snear;   // raw scale bits, converted when the tile is dequantised
+  uint32_t sfar = 0, snear = 0;   // raw scale bits, converted when the tile is dequantised
 
   auto load_b = [&](int k0) {
-    if constexpr (kBWords == 4) bfar = gload_b128(wrow + (k0 >> 1));
-    else bfar2 = gload_b64(wrow + (k0 >> 1));
-    const stype* ps = sp + (k0 + b_part * C::kBBytes * 2) / group;
-    if constexpr (sizeof(stype) == 2) sfar = gload_u16(ps);
-    else sfar = gload_b32(ps);
+    const int kb = WBITS == 4 ? (k0 >> 1) : k0;          // byte offset of k0 in the row
+    if constexpr (kBWords == 4) bfar = gload_b128(wrow + kb);
+    else bfar2 = gload_b64(wrow + kb);
+    if constexpr (!kPost) {
+      const stype* ps = sp + (k0 + b_part * Bg::kSpanK) / group;
+      if constexpr (sizeof(stype) == 2) sfar = gload_u16(ps);
+      else sfar = gload_b32(ps);
+    }
   };
   // WAIT_FAR(n): wait until at most n loads are outstanding; ties the `far`
   // registers so their consumers (and the copy to `near`) stay below it.  A
@@ -166,24 +184,55 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
     const half_t hs = half_t(bs);
     const half2_t s2 = {hs, hs};
     half_t* dst = Bs[stage];
+    if constexpr (WBITS == 4) {
+      // one dword = 8 k = one 16-byte LDS chunk
 #pragma unroll
-    for (int i = 0; i < kBWords; ++i) {
-      half2_t h[4];
-      int4x8_to_h2(bq[i], h);
-      u32x4_t v;
-      v.x = as_u32(h[0] * s2);
-      v.y = as_u32(h[1] * s2);
-      v.z = as_u32(h[2] * s2);
-      v.w = as_u32(h[3] * s2);
-      *reinterpret_cast<u32x4_t*>(dst + b_lds_off(b_n, b_part * kBWords + i)) = v;
+      for (int i = 0; i < kBWords; ++i) {
+        half2_t h[4];
+        int4x8_to_h2(bq[i], h);
+        u32x4_t v;
+        v.x = as_u32(h[0] * s2);
+        v.y = as_u32(h[1] * s2);
+        v.z = as_u32(h[2] * s2);
+        v.w = as_u32(h[3] * s2);
+        *reinterpret_cast<u32x4_t*>(dst + b_lds_off(b_n, b_part * kBWords + i)) = v;
+      }
+    } else {
+      // two dwords = 8 k = one 16-byte LDS chunk of exact integers
+      (void)s2;
+#pragma unroll
+      for (int i = 0; i < kBWords / 2; ++i) {
+        half2_t h[4];
+        int8x4_to_h2(bq[2 * i], h);
+        int8x4_to_h2(bq[2 * i + 1], h + 2);
+        u32x4_t v;
+        v.x = as_u32(h[0]);
+        v.y = as_u32(h[1]);
+        v.z = as_u32(h[2]);
+        v.w = as_u32(h[3]);
+        *reinterpret_cast<u32x4_t*>(dst + b_lds_off(b_n, b_part * (kBWords / 2) + i)) = v;
+      }
     }
   };
 
   float4_t acc[TM][TN];
+  float4_t part[kPost ? TM : 1][kPost ? TN : 1];   // int8: this group's unscaled sums
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (kPost) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) part[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    // stage the tile's scale rows (fp32) before any hand-counted load
+    for (int idx = tid; idx < BN * num_scales; idx += C::kThreads) {
+      const int row = idx / num_scales;
+      const int n = min(n0 + row, N - 1);
+      Ssh[idx] = load_f32<SD>(S, size_t(n) * num_scales + (idx - row * num_scales));
+    }
+  }
 
   const int ksteps = K / kBK;
   // prologue: A(0), A(1) by DMA; B(0) dequantised into LDS; B(1) in `near`
@@ -219,8 +268,29 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
       for (int i = 0; i < TM; ++i) {
         const h8 a = *reinterpret_cast<const h8*>(as_l + a_lds_off(wrow0 + i * 16 + r16, kk * 4 + q4));
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j) {
+          if constexpr (kPost)
+            part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], part[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if constexpr (kPost) {
+      // group ends with this step: acc += part * s[n, g]; part = 0
+      if (((ks + 1) * kBK) % group == 0) {
+        const int g = (ks * kBK) / group;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const float sj = Ssh[((wn * TN + j) * 16 + r16) * num_scales + g];
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            acc[i][j] += part[i][j] * sj;
+            part[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+            // keep the MFMA-result read in this block (see the decode GEMV)
+            __asm__ volatile("" : "+v"(acc[i][j]), "+v"(part[i][j]));
+          }
+        }
       }
     }
 #if LQ_GEMM_VARIANT == 1
@@ -275,30 +345,29 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
 #endif
 typedef GemmCfg<LQ_GEMM_CFG> GemmDefault;   // default: 256 x 128 tile, 8 waves of 32 x 128
 
-template <class C, int SD, int OD>
+template <class C, int WBITS, int SD, int OD>
 static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O, int64_t M,
                            int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const int tiles_m = int((M + C::BM - 1) / C::BM);
   const int tiles_n = int((N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm_w4_kernel<C, SD, OD>), dim3(unsigned(tiles_m * tiles_n)),
+  hipLaunchKernelGGL((gemm_w4_kernel<C, WBITS, SD, OD>), dim3(unsigned(tiles_m * tiles_n)),
                      dim3(C::kThreads), 0, st, static_cast<const half_t*>(X),
                      static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K), int(K / G),
                      int(G), tiles_m, tiles_n);
   return check_launch();
 }
 
-template <int SD, int OD>
+template <int WBITS, int SD, int OD>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, hipStream_t st) {
-  return launch_gemm_cfg<GemmDefault, SD, OD>(X, W, S, O, M, N, K, G, st);
+  return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
 }
 
 template <int WBITS>
 int launch_gemm(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
                 int64_t K, int64_t G, int sd, int od, hipStream_t st) {
-  static_assert(WBITS == 4, "prefill GEMM is int4-only");
 #define LQ_GM(SD_, OD_) \
-  if (sd == SD_ && od == OD_) return launch_gemm_t<SD_, OD_>(X, W, S, O, M, N, K, G, st)
+  if (sd == SD_ && od == OD_) return launch_gemm_t<WBITS, SD_, OD_>(X, W, S, O, M, N, K, G, st)
   LQ_GM(LQ_F16, LQ_F16);
   LQ_GM(LQ_F16, LQ_F32);
   LQ_GM(LQ_F16, LQ_BF16);
@@ -313,6 +382,8 @@ int launch_gemm(const void* X, const void* W, const void* S, void* O, int64_t M,
 }
 
 template int launch_gemm<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
+                            int64_t, int64_t, int, int, hipStream_t);
+template int launch_gemm<8>(const void*, const void*, const void*, void*, int64_t, int64_t,
                             int64_t, int64_t, int, int, hipStream_t);
 
 }  // namespace lq

@@ -171,11 +171,23 @@ def test_matvec_many_rows_and_per_channel(wbits, M, N, K, G):
     _close(got, _oracle(wbits, X, W, S, G))
 
 
-@pytest.mark.parametrize("M,N,K,G", [(96, 160, 256, 128), (130, 64, 512, 32), (256, 256, 1024, 64)])
-def test_matmul_prefill_small(policy, M, N, K, G):
-    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K)
-    got = _matvec(4, X, W, S, N, K, G, "f16")
-    _close(got, _oracle(4, X, W, S, G))
+@pytest.mark.parametrize("wbits", [4, 8])
+@pytest.mark.parametrize("M,N,K,G", [(96, 160, 256, 128), (130, 64, 512, 32), (256, 256, 1024, 64),
+                                     (300, 200, 576, 64)])
+def test_matmul_prefill_small(policy, wbits, M, N, K, G):
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=M + N + K)
+    got = _matvec(wbits, X, W, S, N, K, G, "f16")
+    _close(got, _oracle(wbits, X, W, S, G))
+
+
+def test_int8_prefill_large():
+    """W8A16 prefill (M = 512, 4096 x 4096, G = 128) on the MFMA GEMM."""
+    M, N, K, G = 512, 4096, 4096, 128
+    X, W, S = synth.matvec_case(8, M, N, K, G, 0.002, 0.02, seed=8)
+    got = _matvec(8, X, W, S, N, K, G, "f16")
+    rows = np.r_[0:32, 250:282, M - 32:M]
+    _close(got[rows], _oracle(8, X[rows], W, S, G))
+    assert np.isfinite(got.astype(np.float32)).all()
 
 
 def test_cfg1_w8a32_fp32():
