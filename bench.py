@@ -139,9 +139,12 @@ class Stack:
     (q, k, v, o, gate, up, down) at M = 1, random weights (BASELINE config 5b).
     One step = all 210 GEMVs of one token, launched back to back (in a graph)."""
 
-    def __init__(self, seed=0, G=32, fused=False):
+    def __init__(self, seed=0, G=32, fused=False, silu=False):
         """fused=True concatenates the weights of linears that read the same
-        activation (q|k|v: N = 960, gate|up: N = 3072): 4 GEMVs per layer."""
+        activation (q|k|v: N = 960, gate|up: N = 3072): 4 GEMVs per layer.
+        silu=True (with fused) runs gate|up as the fused SiLU * mul launch
+        (interleaved rows, 1536 outputs), which also covers the reference's
+        separate silu_mul_kernel (examples/54:113-120)."""
         import torch
         from locomp_amd import synth, _lib
         self.lib = _lib.load()
@@ -161,17 +164,23 @@ class Stack:
                 W = synth.int4_weights(rng, N, K)
                 S = synth.scales(rng, N, K // G, 0.001, 0.01)
                 O = torch.empty(N, dtype=torch.float16, device="cuda")
-                self.layers.append((N, K, G, _dev(W), _dev(S), O))
+                epi = silu and fused and N == 2 * 1536
+                self.layers.append((N, K, G, _dev(W), _dev(S), O, epi))
                 self.algo_bytes += W.nbytes + S.nbytes + K * 2 + N * 2
         self.R = 1
         torch.cuda.synchronize()
 
     def launch(self, i, stream):
         vp = ctypes.c_void_p
-        for (N, K, G, W, S, O) in self.layers:
-            rc = self.lib.locomp_amd_dequant_matvec_int4(
-                vp(self.xs[K].data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
-                K, K // 2, K // G, G, N, 1, 1, 1, 1, stream)
+        for (N, K, G, W, S, O, epi) in self.layers:
+            if epi:
+                rc = self.lib.locomp_amd_dequant_matvec_int4_silu_mul(
+                    vp(self.xs[K].data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
+                    K, K // 2, K // G, G, N // 2, 1, 1, 1, 1, stream)
+            else:
+                rc = self.lib.locomp_amd_dequant_matvec_int4(
+                    vp(self.xs[K].data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
+                    K, K // 2, K // G, G, N, 1, 1, 1, 1, stream)
             if rc != 0:
                 raise RuntimeError(f"launch failed: {rc}")
 
@@ -351,14 +360,15 @@ def main():
     if want("quantize"):
         run_case("quantize_int4_4096x4096_g32_from_f32", QuantCase(4096, 4096, 32), "hbm")
     if want("smollm2"):
-        for fused in (False, True):
-            st = Stack(fused=fused)
+        for fused, silu in ((False, False), (True, False), (True, True)):
+            st = Stack(fused=fused, silu=silu)
             tt, nn = time_graph(st, 40, 5, per_graph=4)
             per = tt / nn
             d = {"us_per_token": round(per * 1e6, 2), "GB_s": round(st.algo_bytes / per / 1e9, 1),
                  "gemvs_per_token": len(st.layers), "algorithmic_bytes": st.algo_bytes,
                  "us_per_gemv": round(per * 1e6 / len(st.layers), 3)}
-            name = "smollm2_135m_int4_g32_decode_stack" + ("_qkv_gateup_fused" if fused else "")
+            name = "smollm2_135m_int4_g32_decode_stack" + ("_qkv_gateup_fused" if fused else "") + \
+                ("_silu_epilogue" if silu else "")
             extra[name] = d
             log(name, d)
     if want("w8a16"):

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define LOCOMP_AMD_ABI_VERSION 2
+#define LOCOMP_AMD_ABI_VERSION 3
 
 /* Element dtype codes. */
 enum {
@@ -127,6 +127,20 @@ int locomp_amd_dequant_matvec_int8(const void* X, const void* W,
                                    int64_t GROUP_SIZE, int64_t N, int64_t M,
                                    int x_dtype, int scale_dtype,
                                    int out_dtype, void* stream);
+
+/* SmolLM2-style MLP front half in one launch: W holds the int4 gate and up
+ * projections with their rows interleaved (row 2i = gate_i, row 2i + 1 =
+ * up_i; uint8 [2I, K/2], scales [2I, K/G]) and
+ *     O[m, i] = silu(g) * u,  g = X[m] . deq(W[2i]),  u = X[m] . deq(W[2i + 1]),
+ *     silu(g) = g / (1 + exp(-g)),  O: [M, I].
+ * Replaces two dequant_matvec_int4 launches plus silu_mul_kernel
+ * (examples/54_smollm2_inference.py:113-120, 545-548); arguments as
+ * locomp_amd_dequant_matvec_int4 with I = intermediate size (half the rows). */
+int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const void* scales,
+                                            void* O, int64_t K_dim, int64_t HALF_K,
+                                            int64_t NUM_SCALES, int64_t GROUP_SIZE, int64_t I,
+                                            int64_t M, int x_dtype, int scale_dtype, int out_dtype,
+                                            void* stream);
 
 /* Quantize float weights W [N, K] (in_dtype fp32 / fp16 / bf16) on the GPU
  * into PACKED uint8 [N, K/2] (byte j = q[2j] | q[2j+1] << 4) and float32

@@ -13,7 +13,8 @@ import numpy as _np
 from .tensor import Tensor, bfloat16, empty, ones, tensor, zeros
 from .kernels import (dequant_int4, dequant_int8, dequant_matmul_int4, dequant_matmul_int8,
                       dequant_matvec_int4, dequant_matvec_int8, quant_matvec_int8)
-from .ops import gpu_dequant_int4, gpu_dequant_int8, gpu_matvec_int4, gpu_matvec_int8
+from .ops import (gpu_dequant_int4, gpu_dequant_int8, gpu_matvec_int4, gpu_matvec_int4_silu_mul,
+                  gpu_matvec_int8, interleave_gate_up)
 from .quantize import quantize_int4, quantize_int4_ref, quantize_int8
 from .checkpoint import QuantizedLinear, load_packed, quantize_checkpoint, read_packed, save_packed
 from ._lib import LocompAMDError, get_policy, set_policy
@@ -44,6 +45,7 @@ __all__ = [
     "dequant_int4", "dequant_int8", "dequant_matvec_int4", "dequant_matvec_int8",
     "dequant_matmul_int4", "dequant_matmul_int8", "quant_matvec_int8",
     "gpu_matvec_int4", "gpu_matvec_int8", "gpu_dequant_int4", "gpu_dequant_int8",
+    "gpu_matvec_int4_silu_mul", "interleave_gate_up",
     "quantize_int4", "quantize_int4_ref", "quantize_int8",
     "QuantizedLinear", "quantize_checkpoint", "save_packed", "read_packed", "load_packed",
     "LocompAMDError", "set_policy", "get_policy",

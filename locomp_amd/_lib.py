@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_liblocomp_amd.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # dtype codes (LQ_F32 / LQ_F16 / LQ_BF16)
 F32, F16, BF16 = 0, 1, 2
@@ -40,6 +40,8 @@ SIGNATURES = {
                                        _int, _int, _int, _vp],
     "locomp_amd_dequant_matvec_int8": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                        _int, _int, _int, _vp],
+    "locomp_amd_dequant_matvec_int4_silu_mul": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                                _i64, _int, _int, _int, _vp],
     "locomp_amd_quantize_int4": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp],
     "locomp_amd_quantize_int8": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
 }

@@ -21,6 +21,10 @@ int launch_gemm(const void*, const void*, const void*, void*, int64_t, int64_t, 
 int launch_zero_fill(void*, int64_t, int, hipStream_t);
 int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
                     hipStream_t);
+int launch_silu_fast(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                     int64_t, int, int, hipStream_t);
+int launch_generic_silu(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                        int64_t, int, int, int, hipStream_t);
 
 static std::atomic<int> g_policy{LQ_POLICY_AUTO};
 
@@ -151,6 +155,33 @@ int locomp_amd_dequant_matvec_int8(const void* X, const void* W, const void* sca
   if (rc) return rc;
   return matmul_dispatch<8>(X, W, scales, O, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
                             out_dtype, static_cast<hipStream_t>(stream));
+}
+
+int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const void* scales,
+                                            void* O, int64_t K_dim, int64_t HALF_K,
+                                            int64_t NUM_SCALES, int64_t GROUP_SIZE, int64_t I,
+                                            int64_t M, int x_dtype, int scale_dtype, int out_dtype,
+                                            void* stream) {
+  int rc = check_common(K_dim, NUM_SCALES, GROUP_SIZE, I);
+  if (rc) return rc;
+  if (HALF_K * 2 != K_dim) return LQ_ERR_SHAPE;
+  if (!dtype_ok(x_dtype) || !dtype_ok(scale_dtype) || !dtype_ok(out_dtype)) return LQ_ERR_DTYPE;
+  if (M < 0) return LQ_ERR_SHAPE;
+  if (M == 0 || I == 0) return LQ_OK;
+  if (!O) return LQ_ERR_NULL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K_dim == 0) return launch_zero_fill(O, M * I, out_dtype, st);   // silu(0) * 0
+  if (!X || !W || !scales) return LQ_ERR_NULL;
+  const int64_t N = 2 * I;
+  const bool fast = fast_allowed() && x_dtype == LQ_F16 && aligned(X, 16) && aligned(W, 16) &&
+                    M * K_dim <= kMax32 && N * HALF_K <= kMax32 && N * NUM_SCALES <= kMax32 &&
+                    scale_dtype != LQ_BF16 && out_dtype != LQ_BF16;
+  if (fast) {
+    rc = launch_silu_fast(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
+  return launch_generic_silu(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
+                             out_dtype, st);
 }
 
 // Quantizers.  mode: 0 = examples/38 quantize_int4, 1 = examples/52

@@ -36,6 +36,62 @@ __global__ __launch_bounds__(256) void generic_matvec_kernel(
   }
 }
 
+// Gate|up dequant-matmul with the SiLU * mul epilogue, any shape and dtype:
+// block i computes rows 2i (gate_i) and 2i + 1 (up_i) of the interleaved
+// int4 weights and stores silu(gate_i) * up_i to O [M, N / 2]
+// (examples/54_smollm2_inference.py:113-120, 545-548).
+template <int XD, int SD, int OD>
+__global__ __launch_bounds__(256) void generic_silu_kernel(
+    const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int64_t M, int64_t N, int64_t K, int64_t num_scales, int64_t group) {
+  const int64_t i = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const uint8_t* wg = W + (2 * i) * (K / 2);
+  const uint8_t* wu = wg + K / 2;
+  for (int64_t m = wave; m < M; m += 4) {
+    float ag = 0.f, au = 0.f;
+    for (int64_t k = lane; k < K; k += 64) {
+      const uint32_t bg = wg[k >> 1], bu = wu[k >> 1];
+      const int qg = int((k & 1) ? (bg >> 4) : (bg & 0xFu)) - 8;
+      const int qu = int((k & 1) ? (bu >> 4) : (bu & 0xFu)) - 8;
+      const float x = load_f32<XD>(X, size_t(m * K + k));
+      ag += x * (float(qg) * load_f32<SD>(S, size_t((2 * i) * num_scales + k / group)));
+      au += x * (float(qu) * load_f32<SD>(S, size_t((2 * i + 1) * num_scales + k / group)));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      ag += __shfl_xor(ag, off, 64);
+      au += __shfl_xor(au, off, 64);
+    }
+    if (lane == 0) store_f32<OD>(O, size_t(m * (N / 2) + i), ag / (1.0f + expf(-ag)) * au);
+  }
+}
+
+template <int XD, int SD, int OD>
+static int launch_generic_silu_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                                 int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  hipLaunchKernelGGL((generic_silu_kernel<XD, SD, OD>), dim3(unsigned(N / 2)), dim3(256), 0, st, X,
+                     static_cast<const uint8_t*>(W), S, O, M, N, K, K / G, G);
+  return check_launch();
+}
+
+int launch_generic_silu(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                        int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
+#define LQ_GS(XD_, SD_, OD_) \
+  if (xd == XD_ && sd == SD_ && od == OD_) return launch_generic_silu_t<XD_, SD_, OD_>(X, W, S, O, M, N, K, G, st)
+#define LQ_GS_X(XD_) \
+  LQ_GS(XD_, LQ_F32, LQ_F32); LQ_GS(XD_, LQ_F32, LQ_F16); LQ_GS(XD_, LQ_F32, LQ_BF16); \
+  LQ_GS(XD_, LQ_F16, LQ_F32); LQ_GS(XD_, LQ_F16, LQ_F16); LQ_GS(XD_, LQ_F16, LQ_BF16); \
+  LQ_GS(XD_, LQ_BF16, LQ_F32); LQ_GS(XD_, LQ_BF16, LQ_F16); LQ_GS(XD_, LQ_BF16, LQ_BF16)
+  LQ_GS_X(LQ_F32);
+  LQ_GS_X(LQ_F16);
+  LQ_GS_X(LQ_BF16);
+#undef LQ_GS_X
+#undef LQ_GS
+  return LQ_ERR_DTYPE;
+}
+
 // Writes zeros to O (K == 0: empty reduction).
 template <int OD>
 __global__ void zero_fill_kernel(void* O, int64_t count) {

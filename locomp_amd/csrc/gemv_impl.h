@@ -375,7 +375,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_lds_kernel(
 // transposed butterfly (log2(RW) exchange stages, then 6 - log2(RW) plain
 // stages).  Load order: activations, scales, then all weights, so the
 // in-order vmcnt lets each row start as soon as its own bytes arrive.
-template <int M_, int NSEG, int RW, int SD, int OD>
+// EPI: the weight rows are gate / up interleaved (row 2i = gate_i, 2i + 1 =
+// up_i) and the kernel stores silu(gate_i) * up_i to O [M, N / 2] instead of
+// the N dot products (examples/54_smollm2_inference.py:113-120, 545-548).
+template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false>
 __global__ __launch_bounds__(256, 3) void gemv_rows_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
@@ -509,7 +512,17 @@ __global__ __launch_bounds__(256, 3) void gemv_rows_kernel(
       for (int c2 = RW; c2 > 1; c2 >>= 1, w2 >>= 1) row = row * 2 + ((lane & w2) ? 1 : 0);
     }
     const int lowmask = (64 / RW) - 1;
-    if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+    if constexpr (EPI) {
+      static_assert(RW % 2 == 0, "gate / up pairs within one wave");
+      // row r and r ^ 1 sit in lanes that differ in bit log2(64 / RW)
+      const float other = __shfl_xor(v[0], 64 / RW, 64);
+      if ((lane & lowmask) == 0 && (row & 1) == 0 && m < M && n0 + row + 1 < N) {
+        const float g = v[0];
+        store_f32<OD>(O, size_t(m) * (N >> 1) + ((n0 + row) >> 1), g / (1.0f + expf(-g)) * other);
+      }
+    } else {
+      if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+    }
   }
 }
 
@@ -1277,24 +1290,24 @@ static int launch_gemv_lds_p(const void* X, const void* W, const void* S, void* 
 }
 
 
-template <int M_, int NSEG, int RW, int SD, int OD>
+template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false>
 static int launch_gemv_rows_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                               int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const unsigned blocks = unsigned((N + 4 * RW - 1) / (4 * RW));
-  hipLaunchKernelGGL((gemv_rows_kernel<M_, NSEG, RW, SD, OD>), dim3(blocks), dim3(256), 0, st,
+  hipLaunchKernelGGL((gemv_rows_kernel<M_, NSEG, RW, SD, OD, EPI>), dim3(blocks), dim3(256), 0, st,
                      static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
                      int(N), int(K), int(K / G), int(G));
   return check_launch();
 }
 
-template <int M_, int SD, int OD>
+template <int M_, int SD, int OD, bool EPI = false>
 static int launch_gemv_rows_m(const void* X, const void* W, const void* S, void* O, int64_t M,
                               int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const int64_t nseg = (K + 2047) / 2048;
-  if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, SD, OD>(X, W, S, O, M, N, K, G, st);
-  if (nseg <= 2) return launch_gemv_rows_t<M_, 2, 4, SD, OD>(X, W, S, O, M, N, K, G, st);
-  if (nseg <= 4) return launch_gemv_rows_t<M_, 4, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
-  return launch_gemv_rows_t<M_, 8, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+  if (nseg <= 2) return launch_gemv_rows_t<M_, 2, 4, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+  if (nseg <= 4) return launch_gemv_rows_t<M_, 4, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+  return launch_gemv_rows_t<M_, 8, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
 }
 
 template <int M_, int NSEG, int RW, int SD, int OD>
@@ -1459,6 +1472,23 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
   if (M <= 16) return launch_skinny_mt<WBITS, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
   if (M <= 32) return launch_skinny_mt<WBITS, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
   return launch_skinny_mt<WBITS, 4, SD, OD>(X, W, S, O, M, N, K, G, st);
+}
+
+// Gate|up GEMV with the SiLU * mul epilogue on the row-contiguous kernel
+// (int4, M <= 2, G % 32 == 0).  Returns LQ_ERR_SHAPE when it does not apply.
+inline int launch_rows_silu(const void* X, const void* W, const void* S, void* O, int64_t M,
+                            int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  if (!gemv_rows_ok(4, M, K, G)) return LQ_ERR_SHAPE;
+#define LQ_RS(SD_, OD_)                                                                       \
+  if (sd == SD_ && od == OD_)                                                                 \
+    return M == 1 ? launch_gemv_rows_m<1, SD_, OD_, true>(X, W, S, O, M, N, K, G, st)        \
+                  : launch_gemv_rows_m<2, SD_, OD_, true>(X, W, S, O, M, N, K, G, st)
+  LQ_RS(LQ_F16, LQ_F16);
+  LQ_RS(LQ_F16, LQ_F32);
+  LQ_RS(LQ_F32, LQ_F16);
+  LQ_RS(LQ_F32, LQ_F32);
+#undef LQ_RS
+  return LQ_ERR_SHAPE;
 }
 
 template <int WBITS>

@@ -85,3 +85,45 @@ def gpu_dequant_int8(w_int8, scales, N, K, group_size=32, out_dtype=np.float32):
     result = O_g.numpy().reshape(N, K)
     W_g.free(); S_g.free(); O_g.free()
     return result
+
+
+def interleave_gate_up(gate, up):
+    """Rows of two [I, ...] arrays interleaved into [2I, ...] (gate_i, up_i, ...):
+    the weight / scale layout of ``gpu_matvec_int4_silu_mul``."""
+    gate, up = np.asarray(gate), np.asarray(up)
+    if gate.shape != up.shape:
+        raise ValueError(f"gate {gate.shape} and up {up.shape} differ")
+    out = np.empty((2 * gate.shape[0],) + gate.shape[1:], gate.dtype)
+    out[0::2] = gate
+    out[1::2] = up
+    return out
+
+
+def gpu_matvec_int4_silu_mul(x, w_gate_up, scales, group_size=32, out_dtype=None):
+    """silu(x @ deq(W_gate)^T) * (x @ deq(W_up)^T) in one launch.
+
+    ``w_gate_up`` / ``scales``: gate and up rows interleaved ([2I, K//2] uint8,
+    [2I, K//G]; see ``interleave_gate_up``); x: [K] or [M, K] -> [I] or [M, I].
+    Replaces examples/54_smollm2_inference.py:545-548 (two matvecs and
+    silu_mul_kernel, :113-120)."""
+    from . import _lib
+    from .kernels import _current_stream
+    from .tensor import code_of
+    K = x.shape[-1]
+    N2 = w_gate_up.shape[0]
+    if K % group_size or K % 2 or N2 % 2:
+        raise ValueError(f"K={K} must be even and a multiple of group_size={group_size}; "
+                         f"rows={N2} must be even")
+    I = N2 // 2
+    M = 1 if len(x.shape) == 1 else x.shape[0]
+    xd = _float_dtype_of(x)
+    X_g = _as_dev(x, None if isinstance(x, Tensor) else xd)
+    W_g = _as_dev(w_gate_up, np.uint8)
+    S_g = _as_dev(scales)
+    O_g = empty((M, I) if len(x.shape) == 2 else (I,), out_dtype or xd)
+    rc = _lib.load().locomp_amd_dequant_matvec_int4_silu_mul(
+        X_g.data_ptr, W_g.data_ptr, S_g.data_ptr, O_g.data_ptr, K, K // 2, K // group_size,
+        group_size, I, M, code_of(X_g.dtype), code_of(S_g.dtype), code_of(O_g.dtype),
+        _current_stream())
+    _lib.check(rc, "dequant_matvec_int4_silu_mul")
+    return O_g.numpy()

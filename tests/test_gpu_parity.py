@@ -268,3 +268,31 @@ def test_smollm2_layer_shapes_int4_g32():
         X, W, S = sy.matvec_case(4, 1, N, K, 32, 0.001, 0.01, seed=100 + i)
         got = _matvec(4, X, W, S, N, K, 32, "f16")
         _close(got, _oracle(4, X, W, S, 32))
+
+
+# ------------------------------------------------- fused SiLU * mul (MLP) --
+
+def _silu_mul_oracle(X, Wg, Sg, Wu, Su, G):
+    """silu(g) * u of examples/54_smollm2_inference.py:113-120 in float64 on
+    the oracle's matvecs."""
+    g = np.asarray(ref.fast_numpy_matvec_int4(X, Wg, Sg, G), np.float64)
+    u = np.asarray(ref.fast_numpy_matvec_int4(X, Wu, Su, G), np.float64)
+    return g / (1.0 + np.exp(-g)) * u
+
+
+@pytest.mark.parametrize("M,I,K,G,xd", [
+    (1, 1536, 576, 32, "f16"),      # SmolLM2 gate|up, row-contiguous kernel
+    (2, 100, 576, 32, "f16"),
+    (3, 64, 512, 64, "f16"),        # M > 2: generic kernel
+    (1, 48, 256, 16, "f16"),        # G % 32 != 0: generic kernel
+    (2, 40, 128, 32, "f32"),        # fp32 activations: generic kernel
+])
+def test_matvec_int4_silu_mul(policy, M, I, K, G, xd):
+    dt = np.float16 if xd == "f16" else np.float32
+    Xa, Wg, Sg = synth.matvec_case(4, M, I, K, G, 0.01, 0.05, x_dtype=dt, seed=I + K)
+    _, Wu, Su = synth.matvec_case(4, M, I, K, G, 0.01, 0.05, x_dtype=dt, seed=I + K + 1)
+    W = lq.interleave_gate_up(Wg, Wu)
+    S = lq.interleave_gate_up(Sg, Su)
+    got = lq.gpu_matvec_int4_silu_mul(Xa, W, S, G).astype(np.float64)
+    want = _silu_mul_oracle(Xa, Wg, Sg, Wu, Su, G)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
