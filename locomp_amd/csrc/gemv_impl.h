@@ -1217,6 +1217,174 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   }
 }
 
+// ------------------------------------- decode / verify GEMV, int8, M <= 64 --
+// Same LDS ring as gemv_tile_kernel, for 16 < M <= 64: the activations of a
+// chunk are shared by the whole workgroup, so they are copied to LDS by DMA
+// together with the weights instead of being loaded into each wave's
+// registers.  A chunk is 256 k: T tiles of 16 weight rows x 256 bytes plus
+// 64 activation rows x 512 bytes, both XOR-swizzled by row (16-byte
+// positions) through the source addresses.  A 3-slot ring keeps chunks c + 1
+// and c + 2 in flight; every load is a DMA, so a step's wait is a bare vmcnt.
+// Wave w takes k-range [32 w, 32 w + 32) of the chunk: two 16x16x16 MFMA
+// blocks (exact int8 values in fp16) for each of the 4 x T (activation x
+// weight) tiles; the group scale (G % 32 == 0) is applied in fp32 per chunk.
+constexpr int kXChunkK = 256;
+constexpr int kXSlots = 3;
+
+template <int TILES, int SD, int OD>
+__global__ __launch_bounds__(512, 1) void gemv_tile_x8_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  constexpr int kRows = 16 * TILES;
+  constexpr int kWBytes = kRows * kXChunkK;               // int8: 1 byte per k
+  constexpr int kXBytes = 64 * kXChunkK * 2;              // 64 activation rows, fp16
+  constexpr int kSlotB = kWBytes + kXBytes;
+  constexpr int kSSize = SD == LQ_F32 ? 4 : 2;
+  constexpr int kWDma = kWBytes / 1024 / 8;               // W DMA instructions per wave per chunk
+  constexpr int kXDma = kXBytes / 1024 / 8;               // X DMA instructions per wave per chunk
+  static_assert(kWBytes % 8192 == 0 && kXBytes % 8192 == 0, "whole DMA instructions per wave");
+  static_assert(kXSlots * kSlotB >= 8 * 4 * TILES * 64 * 16, "reduction reuses the ring");
+  static_assert(kXSlots * kSlotB + kTScaleLds / 2 <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kXSlots * kSlotB];
+  __shared__ __attribute__((aligned(16))) uint8_t sl[kTScaleLds / 2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int n0 = blockIdx.x * kRows;
+  const int nchunks = K / kXChunkK;
+
+  // W: instruction i of wave w copies rows 4 (kWDma w + i) .. + 3 (256 B each):
+  // lane L -> row + L / 16, 16-byte position L % 16 = logical chunk ^ (row & 15)
+  const uint8_t* wsrc[kWDma];
+#pragma unroll
+  for (int i = 0; i < kWDma; ++i) {
+    const int row = 4 * (wave * kWDma + i) + (lane >> 4);
+    const int n = min(n0 + row, N - 1);
+    wsrc[i] = W + size_t(n) * K + (((lane & 15) ^ (row & 15)) << 4);
+  }
+  // X: instruction i of wave w copies activation rows 2 (kXDma w + i) .. + 1
+  // (512 B each): lane L -> row + L / 32, position L % 32 = chunk ^ (row & 15)
+  const half_t* xsrc[kXDma];
+#pragma unroll
+  for (int i = 0; i < kXDma; ++i) {
+    const int row = 2 * (wave * kXDma + i) + (lane >> 5);
+    const int m = min(row, M - 1);
+    xsrc[i] = X + size_t(m) * K + ((((lane & 31) ^ (row & 15)) << 4) >> 1);
+  }
+  auto issue = [&](int slot, int c) {
+    uint8_t* base = &ring[slot * kSlotB];
+#pragma unroll
+    for (int i = 0; i < kWDma; ++i)
+      dma16(wsrc[i] + size_t(c) * kXChunkK, base + (wave * kWDma + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < kXDma; ++i)
+      dma16(xsrc[i] + size_t(c) * kXChunkK, base + kWBytes + (wave * kXDma + i) * 1024);
+  };
+  constexpr int kGroup = kWDma + kXDma;
+
+  // scale rows of the workgroup (contiguous; buffer runs to the array's end)
+  {
+    const int rows = min(kRows, N - n0);
+    const uint32_t bytes = uint32_t(rows) * uint32_t(num_scales) * kSSize;
+    const uint32_t avail = uint32_t(N - n0) * uint32_t(num_scales) * kSSize;
+    const uint64_t base = reinterpret_cast<uint64_t>(S) + uint64_t(n0) * num_scales * kSSize;
+    const i32x4_t rsrc = {int(uint32_t(base)), int(uint32_t(base >> 32) & 0xFFFFu), int(avail),
+                          0x00020000};
+    const int ninstr = int((bytes + 1023) >> 10);
+    for (int j = wave; j < ninstr; j += 8)
+      dma16_buf(rsrc, uint32_t(j * 1024 + lane * 16), &sl[j * 1024]);
+  }
+
+  float4_t acc[4][TILES];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) acc[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int slot, int c) {
+    const uint8_t* wl = &ring[slot * kSlotB];
+    const uint8_t* xl = wl + kWBytes;
+    float4_t part[4][TILES];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) part[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      // this lane's 4 k: wave * 32 + f * 16 + q4 * 4
+      const int kb = wave * 32 + f * 16 + q4 * 4;
+      h4 bw[TILES];
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        const int row = t * 16 + r16;
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(
+            wl + row * kXChunkK + ((((kb >> 4) ^ (row & 15))) << 4) + (kb & 15));
+        bw[t] = TileMfma<8>::decode(w, 0u);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = mt * 16 + r16;
+        const int byte = kb * 2;
+        const u32x2_t xv = *reinterpret_cast<const u32x2_t*>(
+            xl + row * (kXChunkK * 2) + ((((byte >> 4) ^ (row & 15))) << 4) + (byte & 15));
+        const h4 xa = __builtin_bit_cast(h4, xv);
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) part[mt][t] = TileMfma<8>::mfma(xa, bw[t], part[mt][t]);
+      }
+    }
+    const int g = (c * kXChunkK + wave * 32) / group;
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const uint8_t* ps = sl + (size_t(t * 16 + r16) * num_scales + g) * kSSize;
+      float sc;
+      if constexpr (SD == LQ_F32) sc = *reinterpret_cast<const float*>(ps);
+      else if constexpr (SD == LQ_F16) sc = float(*reinterpret_cast<const half_t*>(ps));
+      else sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        acc[mt][t] += part[mt][t] * sc;
+        // keep the MFMA-result read in this block (see gemv_tile_kernel)
+        __asm__ volatile("" : "+v"(acc[mt][t]));
+      }
+    }
+  };
+
+  issue(0, 0);
+  if (nchunks > 1) issue(1, 1);
+  if (nchunks > 1) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(kGroup) : "memory");
+  else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    if (c + 2 < nchunks) issue((c + 2) % kXSlots, c + 2);
+    compute(c % kXSlots, c);
+    if (c + 2 < nchunks) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(kGroup) : "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  float4_t* red = reinterpret_cast<float4_t*>(ring);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) red[((wave * 4 + mt) * TILES + t) * 64 + lane] = acc[mt][t];
+  __syncthreads();
+  for (int pidx = wave; pidx < 4 * TILES; pidx += 8) {
+    const int mt = pidx / TILES, t = pidx % TILES;
+    float4_t v = red[(mt * TILES + t) * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) v += red[((w * 4 + mt) * TILES + t) * 64 + lane];
+    const int n = n0 + t * 16 + r16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mt * 16 + q4 * 4 + r;
+      if (m < M && n < N) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+    }
+  }
+}
+
 template <int WAVES, int KSPLIT>
 static size_t gemv_lds_bytes(int64_t M, int64_t K, int64_t num_scales, int ssize, int step) {
   return size_t(M) * (K + 8) * 2 +
@@ -1419,6 +1587,33 @@ static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, 
          (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_count(N, K, G, scale_bytes) > 0;
 }
 
+// int8, 16 < M <= 64 on the activation-in-LDS ring: K % 256, G % 32, fp16
+// activations; T = 2 or 4 tiles (at most one workgroup per CU where T = 2 allows),
+// while the workgroup's scale rows fit 16 KB and the array is whole dwords.
+static int gemv_tile_x8_count(int64_t N, int64_t K, int64_t G, int scale_bytes) {
+  int tiles = (N + 31) / 32 <= 256 ? 2 : 4;     // whole weight DMA instructions per wave: 2 or 4
+  if (tiles == 4 && 64 * (K / G) * scale_bytes > kTScaleLds / 2) tiles = 2;
+  return 32 * (K / G) * scale_bytes <= kTScaleLds / 2 ? tiles : 0;
+}
+static bool gemv_tile_x8_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, int scale_bytes) {
+  return wbits == 8 && M > 16 && M <= 64 && K % kXChunkK == 0 && G % 32 == 0 &&
+         (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_x8_count(N, K, G, scale_bytes) > 0;
+}
+template <int SD, int OD>
+static int launch_gemv_tile_x8(const void* X, const void* W, const void* S, void* O, int64_t M,
+                               int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int tiles = gemv_tile_x8_count(N, K, G, SD == LQ_F32 ? 4 : 2);
+  const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
+#define LQ_TX(T_)                                                                            \
+  hipLaunchKernelGGL((gemv_tile_x8_kernel<T_, SD, OD>), dim3(blocks), dim3(512), 0, st,     \
+                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,   \
+                     int(M), int(N), int(K), int(K / G), int(G))
+  if (tiles == 2) LQ_TX(2);
+  else LQ_TX(4);
+#undef LQ_TX
+  return check_launch();
+}
+
 // The diagonal-MFMA kernel applies to int4, M <= 4, G % 128 == 0, K <= 16384.
 static bool gemv_diag_ok(int wbits, int64_t M, int64_t K, int64_t G) {
   return wbits == 4 && M <= 4 && G % 128 == 0 && K % 128 == 0 && K <= 16384 && K >= 128;
@@ -1444,6 +1639,10 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
   if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
     if (M >= 2 && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
+  }
+  if constexpr (WBITS == 8 && SD != LQ_BF16 && OD != LQ_BF16) {
+    if (gemv_tile_x8_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
+      return launch_gemv_tile_x8<SD, OD>(X, W, S, O, M, N, K, G, st);
   }
   if constexpr (WBITS == 4 && SD != LQ_BF16 && OD != LQ_BF16) {
     if (gemv_seg_ok(WBITS, M, N, K, G)) {
