@@ -87,6 +87,29 @@ def test_quantize_abi_validates_without_a_gpu():
     assert q8(P, P, P, 4, 64, 32, 3, NULL) == _lib.ERR_DTYPE
 
 
+def test_silu_mul_abi_validates_without_a_gpu():
+    lib = _lib.load()
+    f = lib.locomp_amd_dequant_matvec_int4_silu_mul
+    # (X, W, scales, O, K_dim, HALF_K, NUM_SCALES, GROUP_SIZE, I, M, xd, sd, od, stream)
+    assert f(P, P, P, P, 64, 31, 2, 32, 8, 1, 1, 1, 1, NULL) == _lib.ERR_SHAPE   # HALF_K
+    assert f(P, P, P, P, 64, 32, 3, 32, 8, 1, 1, 1, 1, NULL) == _lib.ERR_SHAPE   # NUM_SCALES * G != K
+    assert f(P, P, P, P, 64, 32, 2, 32, 8, -1, 1, 1, 1, NULL) == _lib.ERR_SHAPE  # M < 0
+    assert f(P, P, P, P, 64, 32, 2, 32, 8, 1, 7, 1, 1, NULL) == _lib.ERR_DTYPE
+    assert f(NULL, P, P, P, 64, 32, 2, 32, 8, 1, 1, 1, 1, NULL) == _lib.ERR_NULL
+    assert f(P, P, P, NULL, 64, 32, 2, 32, 8, 1, 1, 1, 1, NULL) == _lib.ERR_NULL
+    assert f(NULL, NULL, NULL, NULL, 64, 32, 2, 32, 0, 1, 1, 1, 1, NULL) == 0    # I = 0: nothing to do
+
+
+def test_interleave_gate_up():
+    import locomp_amd as lq
+    g = np.arange(12, dtype=np.uint8).reshape(3, 4)
+    u = 100 + np.arange(12, dtype=np.uint8).reshape(3, 4)
+    w = lq.interleave_gate_up(g, u)
+    assert w.shape == (6, 4) and np.array_equal(w[0::2], g) and np.array_equal(w[1::2], u)
+    with pytest.raises(ValueError):
+        lq.interleave_gate_up(g, u[:2])
+
+
 def test_check_maps_codes_to_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.ERR_SHAPE, "x")
