@@ -357,10 +357,17 @@ static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O,
   return check_launch();
 }
 
+typedef GemmCfg<4, 2, 2, 4> GemmSmall;     // 128 x 128 tile, 8 waves of 32 x 64
+
 template <int WBITS, int SD, int OD>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, hipStream_t st) {
-  return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
+  // 256-row tiles only when they alone give every CU (256) a tile; below that
+  // (M <= 1024 at N = 4096) 128 x 128 tiles finish sooner.
+  const int64_t big_tiles = ((M + GemmDefault::BM - 1) / GemmDefault::BM) *
+                            ((N + GemmDefault::BN - 1) / GemmDefault::BN);
+  if (big_tiles >= 256) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
+  return launch_gemm_cfg<GemmSmall, WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
 }
 
 template <int WBITS>
