@@ -1217,35 +1217,45 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   }
 }
 
-// ------------------------------------- decode / verify GEMV, int8, M <= 64 --
-// Same LDS ring as gemv_tile_kernel, for 16 < M <= 64: the activations of a
-// chunk are shared by the whole workgroup, so they are copied to LDS by DMA
-// together with the weights instead of being loaded into each wave's
-// registers.  A chunk is 256 k: T tiles of 16 weight rows x 256 bytes plus
-// 64 activation rows x 512 bytes, both XOR-swizzled by row (16-byte
-// positions) through the source addresses.  A 3-slot ring keeps chunks c + 1
-// and c + 2 in flight; every load is a DMA, so a step's wait is a bare vmcnt.
-// Wave w takes k-range [32 w, 32 w + 32) of the chunk: two 16x16x16 MFMA
-// blocks (exact int8 values in fp16) for each of the 4 x T (activation x
-// weight) tiles; the group scale (G % 32 == 0) is applied in fp32 per chunk.
+// ----------------------------- decode / verify GEMV, 16 < M <= 64, all-DMA ring --
+// For 16 < M <= 64 the activations of a chunk are shared by the whole
+// workgroup, so they are copied to LDS by DMA together with the weights
+// instead of being loaded into each wave's registers (the M <= 16 design,
+// whose registers would not hold 4 activation tiles).  A chunk is 256 k:
+// 16 T weight rows (256 bytes int8 / 128 bytes int4 each) plus 64 activation
+// rows x 512 bytes, all XOR-swizzled by row (16-byte positions) through the
+// source addresses.  A 3-slot ring keeps chunks c + 1 and c + 2 in flight;
+// the chunk's DMA instructions are dealt round-robin over the 8 waves, every
+// load is a DMA, so a step's wait is a bare vmcnt of this wave's count.  Wave
+// w takes k [32 w, 32 w + 32) of the chunk for all 4 x T (activation x
+// weight) tiles: int8 two exact 16x16x16 blocks; int4 one 16x16x32 block
+// with the 5-op biased decode, the bias one MFMA per activation tile shared
+// by the T weight tiles.  The group scale (G % 32 == 0) is applied in fp32.
 constexpr int kXChunkK = 256;
 constexpr int kXSlots = 3;
 
-template <int TILES, int SD, int OD>
-__global__ __launch_bounds__(512, 1) void gemv_tile_x8_kernel(
+template <int WBITS, int TILES, int SD, int OD>
+__global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  typedef TileMfma<WBITS> Mf;
+  typedef typename Mf::op_t op_t;
   constexpr int kRows = 16 * TILES;
-  constexpr int kWBytes = kRows * kXChunkK;               // int8: 1 byte per k
+  constexpr int kRowB = kXChunkK * WBITS / 8;             // weight bytes per row per chunk
+  constexpr int kPos = kRowB / 16;                        // 16-byte positions per weight row
+  constexpr int kWBytes = kRows * kRowB;
   constexpr int kXBytes = 64 * kXChunkK * 2;              // 64 activation rows, fp16
   constexpr int kSlotB = kWBytes + kXBytes;
   constexpr int kSSize = SD == LQ_F32 ? 4 : 2;
-  constexpr int kWDma = kWBytes / 1024 / 8;               // W DMA instructions per wave per chunk
-  constexpr int kXDma = kXBytes / 1024 / 8;               // X DMA instructions per wave per chunk
-  static_assert(kWBytes % 8192 == 0 && kXBytes % 8192 == 0, "whole DMA instructions per wave");
-  static_assert(kXSlots * kSlotB >= 8 * 4 * TILES * 64 * 16, "reduction reuses the ring");
-  static_assert(kXSlots * kSlotB + kTScaleLds / 2 <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(16))) uint8_t ring[kXSlots * kSlotB];
+  constexpr int kWInstr = kWBytes / 1024;
+  constexpr int kInstr = kWInstr + kXBytes / 1024;
+  constexpr int kPerWaveMax = (kInstr + 7) / 8;
+  static_assert(kWBytes % 1024 == 0, "whole weight DMA instructions");
+  // the cross-wave sum reuses the ring (sized to hold it)
+  constexpr int kRingB = kXSlots * kSlotB > 8 * 4 * TILES * 1024 ? kXSlots * kSlotB
+                                                                  : 8 * 4 * TILES * 1024;
+  static_assert(kRingB + kTScaleLds / 2 <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kRingB];
   __shared__ __attribute__((aligned(16))) uint8_t sl[kTScaleLds / 2];
 
   const int tid = threadIdx.x;
@@ -1254,36 +1264,51 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_x8_kernel(
   const int r16 = lane & 15;
   const int q4 = lane >> 4;
   const int n0 = blockIdx.x * kRows;
+  const int row_bytes = K * WBITS / 8;
   const int nchunks = K / kXChunkK;
 
-  // W: instruction i of wave w copies rows 4 (kWDma w + i) .. + 3 (256 B each):
-  // lane L -> row + L / 16, 16-byte position L % 16 = logical chunk ^ (row & 15)
-  const uint8_t* wsrc[kWDma];
+  // DMA instruction j = wave + 8 i: j < kWInstr copies weight rows
+  // (1024 / kRowB) j .. (lane L -> row + L / kPos, position L % kPos), else
+  // activation rows 2 (j - kWInstr) .. + 1 (lane L -> row + L / 32, position
+  // L % 32); position p of a row holds logical 16-byte chunk p ^ (row & 15)
+  // (^ (row & (kPos - 1)) for the shorter int4 weight rows).
+  const int my_count = (kInstr - wave + 7) / 8;
+  const uint8_t* src[kPerWaveMax];
+  int dst[kPerWaveMax];
+  bool is_w[kPerWaveMax];
 #pragma unroll
-  for (int i = 0; i < kWDma; ++i) {
-    const int row = 4 * (wave * kWDma + i) + (lane >> 4);
-    const int n = min(n0 + row, N - 1);
-    wsrc[i] = W + size_t(n) * K + (((lane & 15) ^ (row & 15)) << 4);
-  }
-  // X: instruction i of wave w copies activation rows 2 (kXDma w + i) .. + 1
-  // (512 B each): lane L -> row + L / 32, position L % 32 = chunk ^ (row & 15)
-  const half_t* xsrc[kXDma];
-#pragma unroll
-  for (int i = 0; i < kXDma; ++i) {
-    const int row = 2 * (wave * kXDma + i) + (lane >> 5);
-    const int m = min(row, M - 1);
-    xsrc[i] = X + size_t(m) * K + ((((lane & 31) ^ (row & 15)) << 4) >> 1);
+  for (int i = 0; i < kPerWaveMax; ++i) {
+    const int j = min(wave + 8 * i, kInstr - 1);
+    is_w[i] = j < kWInstr;
+    if (j < kWInstr) {
+      const int row = (1024 / kRowB) * j + lane / kPos;
+      const int n = min(n0 + row, N - 1);
+      src[i] = W + size_t(n) * row_bytes + (((lane % kPos) ^ (row & (kPos - 1))) << 4);
+      dst[i] = j * 1024;
+    } else {
+      const int row = 2 * (j - kWInstr) + (lane >> 5);
+      const int m = min(row, M - 1);
+      src[i] = reinterpret_cast<const uint8_t*>(X + size_t(m) * K) + (((lane & 31) ^ (row & 15)) << 4);
+      dst[i] = kWBytes + (j - kWInstr) * 1024;
+    }
   }
   auto issue = [&](int slot, int c) {
     uint8_t* base = &ring[slot * kSlotB];
 #pragma unroll
-    for (int i = 0; i < kWDma; ++i)
-      dma16(wsrc[i] + size_t(c) * kXChunkK, base + (wave * kWDma + i) * 1024);
-#pragma unroll
-    for (int i = 0; i < kXDma; ++i)
-      dma16(xsrc[i] + size_t(c) * kXChunkK, base + kWBytes + (wave * kXDma + i) * 1024);
+    for (int i = 0; i < kPerWaveMax; ++i)
+      if (i < my_count)
+        dma16(src[i] + size_t(c) * (is_w[i] ? kRowB : kXChunkK * 2), base + dst[i]);
   };
-  constexpr int kGroup = kWDma + kXDma;
+  // wait until at most `groups` of this wave's chunk groups are outstanding
+  // (a wave issues kPerWaveMax or kPerWaveMax - 1 DMAs per chunk)
+  auto wait_groups = [&](int groups) {
+    const bool full = my_count == kPerWaveMax;
+    if (groups == 0) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (groups == 1 && full) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(kPerWaveMax) : "memory");
+    else if (groups == 1) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(kPerWaveMax - 1) : "memory");
+    else if (full) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kPerWaveMax) : "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kPerWaveMax - 2) : "memory");
+  };
 
   // scale rows of the workgroup (contiguous; buffer runs to the array's end)
   {
@@ -1298,6 +1323,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_x8_kernel(
       dma16_buf(rsrc, uint32_t(j * 1024 + lane * 16), &sl[j * 1024]);
   }
 
+  const uint32_t magic = opaque_u32(0x64006400u);
   float4_t acc[4][TILES];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
@@ -1308,31 +1334,55 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_x8_kernel(
     const uint8_t* wl = &ring[slot * kSlotB];
     const uint8_t* xl = wl + kWBytes;
     float4_t part[4][TILES];
+    if constexpr (WBITS == 8) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int t = 0; t < TILES; ++t) part[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < TILES; ++t) part[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      // this lane's 4 k: wave * 32 + f * 16 + q4 * 4
-      const int kb = wave * 32 + f * 16 + q4 * 4;
-      h4 bw[TILES];
+      for (int f = 0; f < 2; ++f) {
+        const int kb = wave * 32 + f * 16 + q4 * 4;          // this lane's 4 k (= bytes)
+        op_t bw[TILES];
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) {
+          const int row = t * 16 + r16;
+          const uint32_t w = *reinterpret_cast<const uint32_t*>(
+              wl + row * kRowB + (((kb >> 4) ^ (row & (kPos - 1))) << 4) + (kb & 15));
+          bw[t] = Mf::decode(w, magic);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const int row = mt * 16 + r16;
+          const int byte = kb * 2;
+          const u32x2_t xv = *reinterpret_cast<const u32x2_t*>(
+              xl + row * (kXChunkK * 2) + (((byte >> 4) ^ (row & 15)) << 4) + (byte & 15));
+          const op_t xa = Mf::prep_x(xv);
+#pragma unroll
+          for (int t = 0; t < TILES; ++t) part[mt][t] = Mf::mfma(xa, bw[t], part[mt][t]);
+        }
+      }
+    } else {
+      // one 16x16x32 block: the lane's 8 k are wave * 32 + q4 * 8 .., i.e.
+      // dword q4 of weight chunk `wave` and activation bytes 64 w + 16 q4
+      op_t bw[TILES];
 #pragma unroll
       for (int t = 0; t < TILES; ++t) {
         const int row = t * 16 + r16;
         const uint32_t w = *reinterpret_cast<const uint32_t*>(
-            wl + row * kXChunkK + ((((kb >> 4) ^ (row & 15))) << 4) + (kb & 15));
-        bw[t] = TileMfma<8>::decode(w, 0u);
+            wl + row * kRowB + ((wave ^ (row & (kPos - 1))) << 4) + (q4 << 2));
+        bw[t] = Mf::decode(w, magic);
       }
+      const op_t nb = Mf::neg_bias();
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const int row = mt * 16 + r16;
-        const int byte = kb * 2;
-        const u32x2_t xv = *reinterpret_cast<const u32x2_t*>(
-            xl + row * (kXChunkK * 2) + ((((byte >> 4) ^ (row & 15))) << 4) + (byte & 15));
-        const h4 xa = __builtin_bit_cast(h4, xv);
+        const int chunk = wave * 4 + q4;
+        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(
+            xl + row * (kXChunkK * 2) + ((chunk ^ (row & 15)) << 4));
+        const op_t xa = Mf::prep_x(xv);
+        const float4_t start = Mf::mfma(xa, nb, float4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int t = 0; t < TILES; ++t) part[mt][t] = TileMfma<8>::mfma(xa, bw[t], part[mt][t]);
+        for (int t = 0; t < TILES; ++t) part[mt][t] = Mf::mfma(xa, bw[t], start);
       }
     }
     const int g = (c * kXChunkK + wave * 32) / group;
@@ -1354,14 +1404,12 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_x8_kernel(
 
   issue(0, 0);
   if (nchunks > 1) issue(1, 1);
-  if (nchunks > 1) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(kGroup) : "memory");
-  else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  wait_groups(nchunks > 1 ? 1 : 0);
   __syncthreads();
   for (int c = 0; c < nchunks; ++c) {
     if (c + 2 < nchunks) issue((c + 2) % kXSlots, c + 2);
     compute(c % kXSlots, c);
-    if (c + 2 < nchunks) __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(kGroup) : "memory");
-    else __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_groups(c + 2 < nchunks ? 1 : 0);
     __syncthreads();
   }
 
@@ -1375,7 +1423,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_x8_kernel(
     const int mt = pidx / TILES, t = pidx % TILES;
     float4_t v = red[(mt * TILES + t) * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < 8; ++w) v += red[((w * 4 + mt) * TILES + t) * 64 + lane];
+    for (int w2 = 1; w2 < 8; ++w2) v += red[((w2 * 4 + mt) * TILES + t) * 64 + lane];
     const int n = n0 + t * 16 + r16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1587,29 +1635,42 @@ static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, 
          (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_count(N, K, G, scale_bytes) > 0;
 }
 
-// int8, 16 < M <= 64 on the activation-in-LDS ring: K % 256, G % 32, fp16
-// activations; T = 2 or 4 tiles (at most one workgroup per CU where T = 2 allows),
+// 16 < M <= 64 on the activation-in-LDS ring: K % 256, G % 32, fp16
+// activations; T = 1..4 tiles so the grid is at most one workgroup per CU,
 // while the workgroup's scale rows fit 16 KB and the array is whole dwords.
-static int gemv_tile_x8_count(int64_t N, int64_t K, int64_t G, int scale_bytes) {
-  int tiles = (N + 31) / 32 <= 256 ? 2 : 4;     // whole weight DMA instructions per wave: 2 or 4
-  if (tiles == 4 && 64 * (K / G) * scale_bytes > kTScaleLds / 2) tiles = 2;
-  return 32 * (K / G) * scale_bytes <= kTScaleLds / 2 ? tiles : 0;
+static int gemv_tile_xl_count(int wbits, int64_t N, int64_t K, int64_t G, int scale_bytes) {
+  int tiles = 4;
+  for (int t = 1; t <= 4; ++t)
+    if ((N + 16 * t - 1) / (16 * t) <= 256) { tiles = t; break; }
+  // int4 rows are 128 bytes per chunk: whole 1 KB DMA instructions need T even
+  if (wbits == 4 && (tiles & 1)) ++tiles;
+  while (tiles > 0 && 16 * tiles * (K / G) * scale_bytes > kTScaleLds / 2) tiles -= wbits == 4 ? 2 : 1;
+  return tiles;
 }
-static bool gemv_tile_x8_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, int scale_bytes) {
-  return wbits == 8 && M > 16 && M <= 64 && K % kXChunkK == 0 && G % 32 == 0 &&
-         (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_x8_count(N, K, G, scale_bytes) > 0;
+static bool gemv_tile_xl_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, int scale_bytes) {
+  return M > 16 && M <= 64 && K % kXChunkK == 0 && G % 32 == 0 &&
+         (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_xl_count(wbits, N, K, G, scale_bytes) > 0;
 }
-template <int SD, int OD>
-static int launch_gemv_tile_x8(const void* X, const void* W, const void* S, void* O, int64_t M,
+template <int WBITS, int SD, int OD>
+static int launch_gemv_tile_xl(const void* X, const void* W, const void* S, void* O, int64_t M,
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
-  const int tiles = gemv_tile_x8_count(N, K, G, SD == LQ_F32 ? 4 : 2);
+  const int tiles = gemv_tile_xl_count(WBITS, N, K, G, SD == LQ_F32 ? 4 : 2);
   const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
-#define LQ_TX(T_)                                                                            \
-  hipLaunchKernelGGL((gemv_tile_x8_kernel<T_, SD, OD>), dim3(blocks), dim3(512), 0, st,     \
-                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,   \
+#define LQ_TX(T_)                                                                              \
+  hipLaunchKernelGGL((gemv_tile_xl_kernel<WBITS, T_, SD, OD>), dim3(blocks), dim3(512), 0, st, \
+                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,     \
                      int(M), int(N), int(K), int(K / G), int(G))
-  if (tiles == 2) LQ_TX(2);
-  else LQ_TX(4);
+  if constexpr (WBITS == 8) {
+    switch (tiles) {
+      case 1: LQ_TX(1); break;
+      case 2: LQ_TX(2); break;
+      case 3: LQ_TX(3); break;
+      default: LQ_TX(4); break;
+    }
+  } else {
+    if (tiles == 2) LQ_TX(2);
+    else LQ_TX(4);
+  }
 #undef LQ_TX
   return check_launch();
 }
@@ -1640,9 +1701,9 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
     if (M >= 2 && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
-  if constexpr (WBITS == 8 && SD != LQ_BF16 && OD != LQ_BF16) {
-    if (gemv_tile_x8_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
-      return launch_gemv_tile_x8<SD, OD>(X, W, S, O, M, N, K, G, st);
+  if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
+    if (gemv_tile_xl_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
+      return launch_gemv_tile_xl<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
   if constexpr (WBITS == 4 && SD != LQ_BF16 && OD != LQ_BF16) {
     if (gemv_seg_ok(WBITS, M, N, K, G)) {

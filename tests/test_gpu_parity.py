@@ -160,7 +160,7 @@ def test_matvec_lds_ring_shapes(wbits, M, N, K, G):
 @pytest.mark.parametrize("wbits", [4, 8])
 @pytest.mark.parametrize("M,N,K,G", [
     (17, 64, 1024, 64), (33, 300, 2048, 16), (64, 1000, 4096, 4096), (48, 4100, 1536, 512),
-    (16, 1000, 4096, 4096), (3, 77, 1024, 1024)])
+    (16, 1000, 4096, 4096), (3, 77, 1024, 1024), (32, 11008, 4096, 128), (64, 9000, 768, 32)])
 def test_matvec_many_rows_and_per_channel(wbits, M, N, K, G):
     """Decode/verify sizes up to M = 64 and per-channel / large groups
     (one or few scales per row, whose scale rows are not 16-byte multiples)."""
