@@ -28,9 +28,6 @@
 
 #include "lq_common.h"
 
-#ifndef LQ_GEMM_VARIANT
-#define LQ_GEMM_VARIANT 2
-#endif
 
 namespace lq {
 
@@ -293,26 +290,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
         }
       }
     }
-#if LQ_GEMM_VARIANT == 1
-    __builtin_amdgcn_sched_barrier(0);
-#endif
     store_b(b_stage ^ 1);                      // dequantise B(ks + 1)
-#if LQ_GEMM_VARIANT == 0
-    // Interleave that VALU / LDS-write work between the MFMAs.
-#pragma unroll
-    for (int g = 0; g < 32; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // 2 VALU
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
-#elif LQ_GEMM_VARIANT == 3
-#pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // 4 VALU
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
-#endif
     WAIT_FAR(kADma);                           // B(ks + 2) and A(ks + 1) landed
     FAR_TO_NEAR();
     __syncthreads();

@@ -5,11 +5,14 @@
 // Reference semantics: locomp examples/38_quantized_matmul.py:30-87 (int4)
 // and :94-134 (int8): O[m, n] = sum_k X[m, k] * w[n, k], fp32 accumulation.
 //
-// Kernel choice (launch_skinny_sd_od, fp16 activations):
-//   gemv_seg_kernel   int4, M <= 4, G % 128 == 0, K % 2048 == 0   (headline)
-//   gemv_diag_kernel  int4, M <= 4, G % 128 == 0, K % 128 == 0
-//   gemv_rows_kernel  int4, M <= 2, G % 32 == 0
-//   gemv_lds_kernel   M <= 16, activations + scales staged in LDS
+// Kernel choice (launch_skinny_sd_od, fp16 activations), first that applies:
+//   gemv_tile_kernel    2 <= M <= 16, 512-byte row chunks, weights by DMA
+//                       through an LDS ring, activations in registers
+//   gemv_tile_xl_kernel 16 < M <= 64, K % 256, activations and weights by DMA
+//   gemv_seg_kernel     int4, M <= 4, G % 128 == 0, K % 2048 == 0 (headline M = 1)
+//   gemv_diag_kernel    int4, M <= 4, G % 128 == 0, K % 128 == 0
+//   gemv_rows_kernel    int4, M <= 2, G % 32 == 0 (also the gate|up SiLU epilogue)
+//   gemv_lds_kernel     M <= 16, activations + scales staged in LDS
 //   skinny_mfma_kernel  M <= 64 (and everything the above reject)
 //
 // skinny_mfma_kernel: a workgroup of 4 waves owns 16 weight rows and all M;

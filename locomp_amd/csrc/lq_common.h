@@ -211,17 +211,4 @@ __device__ __forceinline__ u32x4_t gload_b128_cached(const void* g) {
   __asm__ volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(g) : "memory");
   return v;
 }
-// Raw bits of scale i (fp32 word or 16-bit pattern) and their value.
-template <int DT>
-__device__ __forceinline__ uint32_t gload_scale_bits(const void* p, size_t i) {
-  if constexpr (DT == LQ_F32) return gload_b32(static_cast<const float*>(p) + i);
-  else return gload_u16(static_cast<const uint16_t*>(p) + i);
-}
-template <int DT>
-__device__ __forceinline__ float scale_from_bits(uint32_t b) {
-  if constexpr (DT == LQ_F32) return __builtin_bit_cast(float, b);
-  else if constexpr (DT == LQ_F16) return float(__builtin_bit_cast(half_t, uint16_t(b)));
-  else return __builtin_bit_cast(float, b << 16);
-}
-
 }  // namespace lq
