@@ -17,10 +17,13 @@
 //     ks + 2 is loaded into registers during step ks, dequantised during step
 //     ks + 1 to exact fp16 (q - 8) or q times the fp16 scale (one rounding) and written to an
 //     XOR-swizzled LDS tile (2 stages) that every wave reads as the B operand.
-//   * One barrier per step.  The loop's loads are inline asm with hand-placed
-//     s_waitcnt (the compiler would drain vmcnt before every LDS read after an
-//     LDS-DMA); MFMAs use the VGPR-destination form (build flag), which keeps
-//     the accumulators from being copied between VGPRs and AGPRs.
+//   * One barrier per step, in its middle: the MFMA operand fragments of each
+//     32-k half are read from LDS while the other half's MFMAs run (the next
+//     step's first half right after the barrier).  The loop's loads are
+//     inline asm with hand-placed s_waitcnt (the compiler would drain vmcnt
+//     before every LDS read after an LDS-DMA); MFMAs use the VGPR-destination
+//     form (build flag), which keeps the accumulators from being copied
+//     between VGPRs and AGPRs.
 //   * XCD-aware order: consecutive workgroups are dealt round-robin to the 8
 //     XCDs, so the tile sequence is arranged for each XCD to walk one 256-row
 //     block of X (2 MB at K = 4096: it stays in that XCD's 4 MB L2).
@@ -36,9 +39,10 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 constexpr int kBK = 64;
 
 // Tile configuration: WM x WN waves, each owning (16 TM) x (16 TN) outputs.
-template <int WM_, int WN_, int TM_, int TN_>
+// OCC_ = workgroups per CU the register budget is sized for.
+template <int WM_, int WN_, int TM_, int TN_, int OCC_ = 1>
 struct GemmCfg {
-  static constexpr int WM = WM_, WN = WN_, TM = TM_, TN = TN_;
+  static constexpr int WM = WM_, WN = WN_, TM = TM_, TN = TN_, kOcc = OCC_;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int BM = WM * TM * 16;
@@ -77,7 +81,7 @@ constexpr int kGemmScaleFloats = 8192;   // int8 post-scale: BN x (K / G) fp32 s
 constexpr int kBStages = 2;
 
 template <class C, int WBITS, int SD, int OD>
-__global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
+__global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int tiles_m, int tiles_n) {
   constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN;
@@ -244,35 +248,63 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
   FAR_TO_NEAR();
   __syncthreads();
 
+  // MFMA operand fragments of one 32-k half step (kk): lane (r16, q4) holds
+  // k = 8 q4 .. 8 q4 + 7 of that half.  The reads of the next half are issued
+  // before the MFMAs of the current one, so LDS reads overlap the matrix
+  // cores instead of alternating with them.
+  auto read_frags = [&](int a_st, int b_st, int kk, h8 (&fa)[TM], h8 (&fb)[TN]) {
+    const half_t* as_l = As[a_st];
+    const half_t* bs_l = Bs[b_st];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      fb[j] = *reinterpret_cast<const h8*>(bs_l + b_lds_off((wn * TN + j) * 16 + r16, kk * 4 + q4));
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      fa[i] = *reinterpret_cast<const h8*>(as_l + a_lds_off(wrow0 + i * 16 + r16, kk * 4 + q4));
+  };
+  auto mfmas = [&](const h8 (&fa)[TM], const h8 (&fb)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (kPost)
+          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], part[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      }
+  };
+  // loads this thread issues per step besides the A DMA: weights (+ scale)
+  constexpr int kBLoads = kPost ? 1 : 2;
+
+  h8 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  read_frags(0, 0, 0, fa0, fb0);
   int a_stage = 0;
   for (int ks = 0; ks < ksteps; ++ks) {
     const int b_stage = ks & 1;
+    const int a_next = a_stage == 2 ? 0 : a_stage + 1;
     const int a_next2 = a_stage == 0 ? 2 : a_stage - 1;   // (a_stage + 2) % 3
     // Issue B(ks + 2) then A(ks + 2) (branch-free: past the end they re-read
-    // the last step and land in buffers no one reads).
+    // the last step and land in buffers no one reads).  A stage (ks + 2) % 3
+    // and B stage (ks + 1) % 2 were last read in step ks - 1, before its
+    // middle barrier.
     const int k2 = min(ks + 2, ksteps - 1) * kBK;
     load_b(k2);
     dma_a(a_next2, k2);
-    const half_t* as_l = As[a_stage];
-    const half_t* bs_l = Bs[b_stage];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      h8 b[TN];
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        b[j] = *reinterpret_cast<const h8*>(bs_l + b_lds_off((wn * TN + j) * 16 + r16, kk * 4 + q4));
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const h8 a = *reinterpret_cast<const h8*>(as_l + a_lds_off(wrow0 + i * 16 + r16, kk * 4 + q4));
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          if constexpr (kPost)
-            part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], part[i][j], 0, 0, 0);
-          else
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], acc[i][j], 0, 0, 0);
-        }
-      }
-    }
+    // The scheduling barriers keep each half's fragment reads ahead of the
+    // other half's MFMAs (the scheduler would otherwise sink them to their use).
+    read_frags(a_stage, b_stage, 1, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa0, fb0);
+    store_b(b_stage ^ 1);                      // dequantise B(ks + 1)
+    __builtin_amdgcn_sched_barrier(0);
+    // A(ks + 1) landed (only this step's loads may remain) and B(ks + 1) is
+    // in LDS for every wave: the next step's first half can be read.
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kBLoads + kADma) : "memory");
+    __syncthreads();
+    read_frags(a_next, b_stage ^ 1, 0, fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (kPost) {
       // group ends with this step: acc += part * s[n, g]; part = 0
       if (((ks + 1) * kBK) % group == 0) {
@@ -290,11 +322,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_w4_kernel(
         }
       }
     }
-    store_b(b_stage ^ 1);                      // dequantise B(ks + 1)
-    WAIT_FAR(kADma);                           // B(ks + 2) and A(ks + 1) landed
+    WAIT_FAR(kADma);                           // B(ks + 2) landed
     FAR_TO_NEAR();
-    __syncthreads();
-    a_stage = a_stage == 2 ? 0 : a_stage + 1;
+    a_stage = a_next;
   }
 
 #undef WAIT_FAR
