@@ -27,7 +27,9 @@
 //   * XCD-aware order: consecutive workgroups are dealt round-robin to the 8
 //     XCDs, so the tile sequence is arranged for each XCD to walk one 256-row
 //     block of X (2 MB at K = 4096: it stays in that XCD's 4 MB L2).
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "lq_common.h"
 
@@ -83,7 +85,8 @@ constexpr int kBStages = 2;
 template <class C, int WBITS, int SD, int OD>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
-    void* __restrict__ O, int M, int N, int K, int num_scales, int group, int tiles_m, int tiles_n) {
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group, int tiles_m, int tiles_n,
+    int kspan) {
   constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN;
   static_assert(BM % (8 * C::kWaves) == 0, "A DMA: whole 1 KB instructions per wave");
   typedef typename Elem<SD>::T stype;
@@ -111,6 +114,10 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   const int m0 = (t / tiles_n) * BM;
   const int n0 = (t % tiles_n) * BN;
   const int row_bytes = WBITS == 4 ? (K >> 1) : K;
+  // split-K: workgroup row blockIdx.y covers k in [kbeg, kbeg + kspan) and
+  // writes its fp32 partial sums to slice blockIdx.y of O
+  const int kbeg = blockIdx.y * kspan;
+  const size_t obase = size_t(blockIdx.y) * M * N;
   const int wrow0 = wm * TM * 16;              // first tile row this wave multiplies
 
   // A DMA: wave w copies rows [w * kDmaRows, (w + 1) * kDmaRows) of the tile
@@ -126,7 +133,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const int row = drow0 + 8 * i + (lane >> 3);
     const int m = min(m0 + row, M - 1);
     const int c = (lane & 7) ^ (row & 7);
-    adma_src[i] = X + size_t(m) * K + c * 8;
+    adma_src[i] = X + size_t(m) * K + kbeg + c * 8;
   }
   auto dma_a = [&](int stage, int k0) {
 #pragma unroll
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   const int b_n = tid / kPerRow;
   const int b_part = tid % kPerRow;
   const int bn = min(n0 + b_n, N - 1);
-  const uint8_t* wrow = W + size_t(bn) * row_bytes + b_part * Bg::kBytes;
+  const uint8_t* wrow = W + size_t(bn) * row_bytes + (WBITS == 4 ? (kbeg >> 1) : kbeg) + b_part * Bg::kBytes;
   const stype* sp = static_cast<const stype*>(S) + size_t(bn) * num_scales;
   constexpr int kBWords = Bg::kBytes / 4;
   // Packed weights: `bfar` receives the loads of step ks + 2 during step ks;
@@ -155,7 +162,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     if constexpr (kBWords == 4) bfar = gload_b128(wrow + kb);
     else bfar2 = gload_b64(wrow + kb);
     if constexpr (!kPost) {
-      const stype* ps = sp + (k0 + b_part * Bg::kSpanK) / group;
+      const stype* ps = sp + (kbeg + k0 + b_part * Bg::kSpanK) / group;
       if constexpr (sizeof(stype) == 2) sfar = gload_u16(ps);
       else sfar = gload_b32(ps);
     }
@@ -228,14 +235,16 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #pragma unroll
       for (int j = 0; j < TN; ++j) part[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
     // stage the tile's scale rows (fp32) before any hand-counted load
-    for (int idx = tid; idx < BN * num_scales; idx += C::kThreads) {
-      const int row = idx / num_scales;
+    // (this split's groups only: kspan is a multiple of the group size)
+    const int ns = kspan / group, g0 = kbeg / group;
+    for (int idx = tid; idx < BN * ns; idx += C::kThreads) {
+      const int row = idx / ns;
       const int n = min(n0 + row, N - 1);
-      Ssh[idx] = load_f32<SD>(S, size_t(n) * num_scales + (idx - row * num_scales));
+      Ssh[idx] = load_f32<SD>(S, size_t(n) * num_scales + g0 + (idx - row * ns));
     }
   }
 
-  const int ksteps = K / kBK;
+  const int ksteps = kspan / kBK;
   // prologue: A(0), A(1) by DMA; B(0) dequantised into LDS; B(1) in `near`
   dma_a(0, 0);
   dma_a(1, min(1, ksteps - 1) * kBK);
@@ -311,7 +320,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
         const int g = (ks * kBK) / group;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const float sj = Ssh[((wn * TN + j) * 16 + r16) * num_scales + g];
+          const float sj = Ssh[((wn * TN + j) * 16 + r16) * (kspan / group) + g];
 #pragma unroll
           for (int i = 0; i < TM; ++i) {
             acc[i][j] += part[i][j] * sj;
@@ -342,7 +351,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int n = n0 + (wn * TN + j) * 16 + r16;
-        if (n < N) store_f32<OD>(O, size_t(m) * N + n, acc[i][j][r]);
+        if (n < N) store_f32<OD>(O, obase + size_t(m) * N + n, acc[i][j][r]);
       }
     }
   }
@@ -355,27 +364,118 @@ typedef GemmCfg<LQ_GEMM_CFG> GemmDefault;   // default: 256 x 128 tile, 8 waves 
 
 template <class C, int WBITS, int SD, int OD>
 static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O, int64_t M,
-                           int64_t N, int64_t K, int64_t G, hipStream_t st) {
+                           int64_t N, int64_t K, int64_t G, int splits, hipStream_t st) {
   const int tiles_m = int((M + C::BM - 1) / C::BM);
   const int tiles_n = int((N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm_w4_kernel<C, WBITS, SD, OD>), dim3(unsigned(tiles_m * tiles_n)),
+  hipLaunchKernelGGL((gemm_w4_kernel<C, WBITS, SD, OD>), dim3(unsigned(tiles_m * tiles_n), unsigned(splits)),
                      dim3(C::kThreads), 0, st, static_cast<const half_t*>(X),
                      static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K), int(K / G),
-                     int(G), tiles_m, tiles_n);
+                     int(G), tiles_m, tiles_n, int(K / splits));
   return check_launch();
 }
 
 typedef GemmCfg<4, 2, 2, 4> GemmSmall;     // 128 x 128 tile, 8 waves of 32 x 64
 
+// ------------------------------------------------------------- split-K --
+// Fewer output tiles than CUs (M < 1024 at N = 4096): the k range is split
+// over up to 8 workgroups per tile, each writing fp32 partial sums to a
+// workspace slice [s][M][N]; split_reduce_kernel adds the slices in order and
+// converts.  The workspace is cached per (device, stream) and only grows; a
+// buffer is never freed while the process runs (a captured graph may still
+// name it), and a call on a capturing stream that would need a larger one
+// runs unsplit instead.  Calls on one stream are ordered; different streams
+// have different workspaces.
+constexpr size_t kSplitWsMax = size_t(256) << 20;
+
+struct SplitWs {
+  int dev;
+  hipStream_t st;
+  void* p;
+  size_t bytes;
+};
+static std::mutex g_ws_mu;
+static std::vector<SplitWs> g_ws;
+
+static void* split_workspace(size_t bytes, hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  for (SplitWs& w : g_ws)
+    if (w.dev == dev && w.st == st && w.bytes >= bytes) return w.p;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  size_t sz = size_t(1) << 20;
+  while (sz < bytes) sz <<= 1;
+  void* p = nullptr;
+  if (hipMalloc(&p, sz) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  for (SplitWs& w : g_ws)
+    if (w.dev == dev && w.st == st) {   // grown: the old buffer stays allocated
+      w.p = p;
+      w.bytes = sz;
+      return p;
+    }
+  g_ws.push_back(SplitWs{dev, st, p, sz});
+  return p;
+}
+
+template <int OD>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ P,
+                                                           void* __restrict__ O, size_t mn,
+                                                           int splits) {
+  const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= mn) return;
+  if (i + 4 <= mn && (mn & 3) == 0) {
+    float4_t a = *reinterpret_cast<const float4_t*>(P + i);
+    for (int s = 1; s < splits; ++s) a += *reinterpret_cast<const float4_t*>(P + size_t(s) * mn + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_f32<OD>(O, i + e, a[e]);
+  } else {
+    for (size_t e = i; e < i + 4 && e < mn; ++e) {
+      float a = P[e];
+      for (int s = 1; s < splits; ++s) a += P[size_t(s) * mn + e];
+      store_f32<OD>(O, e, a);
+    }
+  }
+}
+
+// Number of k splits for `tiles` output tiles: the largest of 8, 6, 4, 3, 2
+// that keeps tiles x splits <= 256 (one workgroup per CU), divides the 64-k
+// steps into runs of >= 4 and, for int8, keeps whole scale groups together.
+template <int WBITS>
+static int choose_splits(int64_t tiles, int64_t K, int64_t G) {
+  const int64_t ksteps = K / kBK;
+  for (int s : {8, 6, 4, 3, 2}) {
+    if (tiles * s > 256 || ksteps % s != 0 || ksteps / s < 4) continue;
+    if (WBITS == 8 && (K / s) % G != 0) continue;
+    return s;
+  }
+  return 1;
+}
+
 template <int WBITS, int SD, int OD>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, hipStream_t st) {
   // 256-row tiles only when they alone give every CU (256) a tile; below that
-  // (M <= 1024 at N = 4096) 128 x 128 tiles finish sooner.
+  // (M <= 1024 at N = 4096) 128 x 128 tiles finish sooner, split over k when
+  // they too leave CUs idle.
   const int64_t big_tiles = ((M + GemmDefault::BM - 1) / GemmDefault::BM) *
                             ((N + GemmDefault::BN - 1) / GemmDefault::BN);
-  if (big_tiles >= 256) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
-  return launch_gemm_cfg<GemmSmall, WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if (big_tiles >= 256) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
+  const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
+                        ((N + GemmSmall::BN - 1) / GemmSmall::BN);
+  const int splits = choose_splits<WBITS>(tiles, K, G);
+  const size_t mn = size_t(M) * size_t(N);
+  const size_t ws_bytes = mn * sizeof(float) * size_t(splits);
+  void* ws = splits > 1 && ws_bytes <= kSplitWsMax ? split_workspace(ws_bytes, st) : nullptr;
+  if (ws == nullptr) return launch_gemm_cfg<GemmSmall, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
+  int rc = launch_gemm_cfg<GemmSmall, WBITS, SD, LQ_F32>(X, W, S, ws, M, N, K, G, splits, st);
+  if (rc != LQ_OK) return rc;
+  hipLaunchKernelGGL((split_reduce_kernel<OD>), dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, st,
+                     static_cast<const float*>(ws), O, mn, splits);
+  return check_launch();
 }
 
 template <int WBITS>

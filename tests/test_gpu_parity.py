@@ -190,6 +190,50 @@ def test_int8_prefill_large():
     assert np.isfinite(got.astype(np.float32)).all()
 
 
+# Split-K prefill (fewer 128 x 128 output tiles than CUs): k split 8, 6, 4
+# ways, fp32 partial slices reduced in order; odd M x N takes the scalar tail
+# of the reduction.  Cases run back to back, so the cached workspace grows.
+@pytest.mark.parametrize("wbits,M,N,K,G,od", [
+    (4, 67, 301, 1024, 64, "f16"),       # 3 tiles, 4 splits, odd M x N
+    (4, 100, 640, 1536, 32, "f32"),      # 5 tiles, 6 splits
+    (8, 100, 640, 1536, 128, "f16"),     # int8: 6 splits of 256 k (whole groups)
+    (4, 128, 4096, 4096, 128, "f16"),    # 32 tiles, 8 splits
+    (8, 128, 4096, 4096, 128, "f32"),
+    (4, 300, 2048, 2048, 128, "f16"),    # 48 tiles, 4 splits
+])
+def test_matmul_prefill_split_k(wbits, M, N, K, G, od):
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=M * 7 + N + K)
+    got = _matvec(wbits, X, W, S, N, K, G, od)
+    _close(got, _oracle(wbits, X, W, S, G), fp32=False)
+
+
+def test_matmul_prefill_split_k_graph():
+    """Split-K GEMM + reduction captured in a graph: every replay (with eager
+    work and synchronisations between them) matches the eager result."""
+    import torch
+    M, N, K, G = 96, 1024, 2048, 128
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=3)
+    Xg, Wg, Sg = _up(X), _up(W), _up(S)
+    Og = lq.empty((M, N), np.float16)
+    run = lambda: lq.dequant_matvec_int4[(N,), (128,)](Xg, Wg, Sg, Og, K, K // 2, K // G, G)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        run()                                     # eager: sizes the workspace
+    torch.cuda.synchronize()
+    eager = Og.numpy().copy()
+    _close(eager, _oracle(4, X, W, S, G))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        run()
+    for _ in range(3):
+        Og.torch.fill_(0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(Og.numpy(), eager)
+
+
 def test_cfg1_w8a32_fp32():
     c = synth.CFG1
     X, W, S = synth.matvec_case(8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
