@@ -106,7 +106,10 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * examples/38_quantized_matmul.py:30-87 (args X, W, scales, O, K_dim, HALF_K,
  * NUM_SCALES, GROUP_SIZE; grid (N,), launched at
  * examples/38_quantized_matmul.py:154).  M = 1 is the reference's matvec;
- * M <= 64 runs the decode (skinny) kernel, larger M the prefill MFMA GEMM. */
+ * M <= 64 runs the decode (skinny) kernel, larger M the prefill MFMA GEMM.
+ * A prefill GEMM with fewer output tiles than CUs splits K and keeps an fp32
+ * workspace per (device, stream), allocated on first use and held until the
+ * process ends (int4 and int8 alike). */
 int locomp_amd_dequant_matvec_int4(const void* X, const void* W,
                                    const void* scales, void* O,
                                    int64_t K_dim, int64_t HALF_K,
