@@ -349,6 +349,11 @@ def main():
         run_case("gemm_prefill_w8a16_2048x4096x4096_g128",
                  Case("matvec", 8, c["M"], c["N"], c["K"], c["G"], 0.002, 0.02,
                       min_bytes=0, max_replicas=4), "mfma")
+    if want("gemm_prefill_small"):
+        c = synth.CFG5A
+        for M in (128, 512):      # split-K shapes (fewer output tiles than CUs)
+            run_case(f"gemm_prefill_w4a16_{M}x4096x4096_g128",
+                     Case("matvec", 4, M, c["N"], c["K"], c["G"], c["lo"], c["hi"]), "mfma")
     for M in (4, 16):
         if want(f"gemv_m{M}"):
             run_case(f"gemv_w4a16_M{M}", Case("matvec", 4, M, c3["N"], c3["K"], c3["G"], c3["lo"],
