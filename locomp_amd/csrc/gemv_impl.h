@@ -721,16 +721,21 @@ __global__ __launch_bounds__(256, 2) void gemv_diag_kernel(
 }
 
 
-// --------------------- decode GEMV, MFMA diagonal, whole 2048-k segments --
-// Same scheme as gemv_diag_kernel, specialised to K % 2048 == 0 with the
-// overhead removed:
+// --------------------------- decode GEMV, MFMA diagonal, 2048-k segments --
+// Same scheme as gemv_diag_kernel with the overhead removed:
 //   * buffer loads (SGPR resource, 32-bit lane offsets, row offset in the
 //     scalar operand); rows past N read as zeros;
 //   * the bias correction is computed by 4 MFMAs per segment (A = the lane's
 //     activations, B = the bias constants 1032 / 1152) and enters each row's
 //     MFMA chain as its initial accumulator (negated), so the chain ends
 //     holding x . (q - 8) directly;
-//   * the diagonal is selected once per (row, segment), scaled, summed.
+//   * the diagonal is selected once per (row, segment), scaled, summed;
+//   * a last, partial segment (K % 2048 != 0, K % 128 == 0) takes buffer
+//     offsets past the end for k >= K: activations, weights and scales read
+//     as zeros there (and cost no memory traffic), so those k add nothing.
+// lane offset past every buffer's end (sizes < 2^31 - 2^30 are checked on the host)
+constexpr int kSegOob = 0x40000000;
+
 template <int M_, int NSEG, int RW, int SD, int OD>
 __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
@@ -762,7 +767,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 #pragma unroll
       for (int c = 0; c < NSEG; ++c)
         xv2[m][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-            rx, ((m * K + c * 2048 + tpos * 32 + te * 8) * 2), 0, 0));
+            rx, c * 2048 + tpos * 32 < K ? (m * K + c * 2048 + tpos * 32 + te * 8) * 2 : kSegOob, 0, 0));
   }
   // 2. scales
   uint32_t sv[RW][NSEG];
@@ -770,11 +775,12 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   for (int r = 0; r < RW; ++r)
 #pragma unroll
     for (int c = 0; c < NSEG; ++c) {
+      const bool kin = c * 2048 + pos * 32 < K;
       const int g = (c * 2048 + pos * 32) / group;
       if constexpr (sizeof(stype) == 2)
-        sv[r][c] = __builtin_amdgcn_raw_buffer_load_b16(rs, g * 2, ((n0 + r) * num_scales) * 2, 0);
+        sv[r][c] = __builtin_amdgcn_raw_buffer_load_b16(rs, kin ? g * 2 : kSegOob, ((n0 + r) * num_scales) * 2, 0);
       else
-        sv[r][c] = __builtin_amdgcn_raw_buffer_load_b32(rs, g * 4, ((n0 + r) * num_scales) * 4, 0);
+        sv[r][c] = __builtin_amdgcn_raw_buffer_load_b32(rs, kin ? g * 4 : kSegOob, ((n0 + r) * num_scales) * 4, 0);
     }
   __builtin_amdgcn_sched_barrier(0);
   // 3. weights
@@ -784,7 +790,8 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 #pragma unroll
     for (int c = 0; c < NSEG; ++c)
       wv[r][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-          rw, c * 1024 + pos * 16, (n0 + r) * half_k, 2 /* nontemporal */));
+          rw, c * 2048 + pos * 32 < K ? c * 1024 + pos * 16 : kSegOob, (n0 + r) * half_k,
+          2 /* nontemporal */));
   __builtin_amdgcn_sched_barrier(0);
 
   // 4. activation operands and bias accumulators, built once per workgroup
@@ -1563,21 +1570,28 @@ static int launch_gemv_seg_t(const void* X, const void* W, const void* S, void* 
 template <int M_, int SD, int OD>
 static int launch_gemv_seg_m(const void* X, const void* W, const void* S, void* O, int64_t M,
                              int64_t N, int64_t K, int64_t G, hipStream_t st) {
-  const int64_t nseg = K / 2048;
+  const int64_t nseg = (K + 2047) / 2048;
   constexpr int rw = M_ <= 2 ? 4 : 2;
   if (nseg == 1) return launch_gemv_seg_t<M_, 1, rw * 2, SD, OD>(X, W, S, O, M, N, K, G, st);
   if (nseg == 2) return launch_gemv_seg_t<M_, 2, rw, SD, OD>(X, W, S, O, M, N, K, G, st);
-  if (nseg <= 4) return launch_gemv_seg_t<M_, 4, (rw > 2 ? rw / 2 : 1), SD, OD>(X, W, S, O, M, N, K, G, st);
-  return launch_gemv_seg_t<M_, 8, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if constexpr (M_ <= 2) {
+    if (nseg <= 4) return launch_gemv_seg_t<M_, 4, (rw > 2 ? rw / 2 : 1), SD, OD>(X, W, S, O, M, N, K, G, st);
+  }
+  if constexpr (M_ == 1) return launch_gemv_seg_t<M_, 8, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+  return LQ_ERR_SHAPE;   // excluded by gemv_seg_ok
 }
 
-// The whole-segment kernel: int4, M <= 4, G % 128 == 0, K % 2048 == 0 with
-// K / 2048 in {1, 2, 4, 8}; byte sizes within the buffer-offset range.
+// The segment kernel: int4, M <= 4, G % 128 == 0, 2048 <= K <= 16384
+// (K / 2048 rounded up to 1, 2, 4 or 8 segments, the last possibly partial),
+// at most 8 (activation row, segment) pairs per lane (more spill registers);
+// buffer sizes plus the out-of-range offset within 32 bits.
 static bool gemv_seg_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G) {
-  const int64_t nseg = K / 2048;
-  return wbits == 4 && M <= 4 && G % 128 == 0 && K % 2048 == 0 &&
-         (nseg == 1 || nseg == 2 || nseg == 4 || nseg == 8) && N * (K / 2) < (int64_t(1) << 31) &&
-         M * K * 2 < (int64_t(1) << 31) && N * (K / G) * 4 < (int64_t(1) << 31);
+  const int64_t lim = (int64_t(1) << 31) - kSegOob;
+  const int64_t nseg = (K + 2047) / 2048;
+  const int64_t segs = nseg <= 1 ? 1 : nseg <= 2 ? 2 : nseg <= 4 ? 4 : 8;
+  const int64_t mrows = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+  return wbits == 4 && M <= 4 && G % 128 == 0 && K % G == 0 && K >= 2048 && K <= 16384 &&
+         mrows * segs <= 8 && N * (K / 2) < lim && M * K * 2 < lim && N * (K / G) * 4 < lim;
 }
 
 // Tiles per workgroup for the LDS-ring kernel: the smallest count whose grid
@@ -1679,14 +1693,19 @@ static int launch_gemv_tile_xl(const void* X, const void* W, const void* S, void
 }
 
 // The diagonal-MFMA kernel applies to int4, M <= 4, G % 128 == 0, K <= 16384.
+// Register budget: the (activation row, segment) pairs a lane holds stay
+// within what compiles without spills (at most 4 for M <= 2, 2 for M <= 4).
 static bool gemv_diag_ok(int wbits, int64_t M, int64_t K, int64_t G) {
-  return wbits == 4 && M <= 4 && G % 128 == 0 && K % 128 == 0 && K <= 16384 && K >= 128;
+  const int64_t nseg = (K + 2047) / 2048;
+  return wbits == 4 && M <= 4 && G % 128 == 0 && K % 128 == 0 && K <= 16384 && K >= 128 &&
+         (M <= 1 || (M <= 2 ? nseg <= 2 : nseg <= 1));
 }
 
 // The row-contiguous kernel applies to int4, M <= 2, K % 32 == 0, G % 32 == 0,
 // K <= 16384.
 static bool gemv_rows_ok(int wbits, int64_t M, int64_t K, int64_t G) {
-  return wbits == 4 && M <= 2 && K % 32 == 0 && G % 32 == 0 && K <= 16384 && K >= 32;
+  return wbits == 4 && M <= 2 && K % 32 == 0 && G % 32 == 0 && K >= 32 &&
+         K <= (M == 1 ? 8192 : 2048);
 }
 
 template <int WBITS, int MT, int SD, int OD>

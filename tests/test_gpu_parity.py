@@ -190,6 +190,23 @@ def test_int8_prefill_large():
     assert np.isfinite(got.astype(np.float32)).all()
 
 
+# Decode (M <= 4) with K not a multiple of 2048: the 2048-k segment kernel
+# with a partial last segment (k >= K read as zeros through out-of-range
+# buffer offsets).
+@pytest.mark.parametrize("M,N,K,G", [
+    (1, 4096, 11008, 128),    # LLaMA-7B down projection, 5.375 segments
+    (1, 333, 2176, 128),      # 1 full + 128-k segment, ragged N
+    (2, 640, 11008, 128),
+    (3, 96, 6144, 256),
+    (4, 257, 14336, 128),     # 7 segments -> 8
+    (1, 100, 3200, 640),
+])
+def test_matvec_int4_partial_segment(M, N, K, G):
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K)
+    got = _matvec(4, X, W, S, N, K, G, "f16")
+    _close(got, _oracle(4, X, W, S, G))
+
+
 # Split-K prefill (fewer 128 x 128 output tiles than CUs): k split 8, 6, 4
 # ways, fp32 partial slices reduced in order; odd M x N takes the scalar tail
 # of the reduction.  Cases run back to back, so the cached workspace grows.
