@@ -71,11 +71,14 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
       return launch_skinny<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
     // Prefill MFMA GEMM: each loader thread's 32 k (int4) / 16 k (int8)
     // inside one group.
-    // int8 post-scales per group: whole 64-k steps per group, and the tile's
-    // 128 scale rows in 8192 fp32 of LDS.
-    const bool gemm_ok = WBITS == 4 ? G % 32 == 0 : (G % 64 == 0 && 128 * (K / G) <= 8192);
-    if (M > 64 && K % 64 == 0 && gemm_ok)
-      return launch_gemm<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
+    // int8 post-scales per group: whole 64-k steps per group (scale rows
+    // beyond what LDS holds split K; a shape no split fits, or a capturing
+    // stream without the workspace that needs, takes the generic kernel).
+    const bool gemm_ok = WBITS == 4 ? G % 32 == 0 : G % 64 == 0;
+    if (M > 64 && K % 64 == 0 && gemm_ok) {
+      const int rc = launch_gemm<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
+      if (rc != LQ_ERR_SHAPE) return rc;
+    }
   }
   return launch_generic<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st);
 }

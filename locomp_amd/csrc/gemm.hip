@@ -27,6 +27,7 @@
 //   * XCD-aware order: consecutive workgroups are dealt round-robin to the 8
 //     XCDs, so the tile sequence is arranged for each XCD to walk one 256-row
 //     block of X (2 MB at K = 4096: it stays in that XCD's 4 MB L2).
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -235,8 +236,9 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #pragma unroll
       for (int j = 0; j < TN; ++j) part[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
     // stage the tile's scale rows (fp32) before any hand-counted load
-    // (this split's groups only: kspan is a multiple of the group size)
-    const int ns = kspan / group, g0 = kbeg / group;
+    // (the groups this split touches: g0 .. g0 + ns - 1; a group may start
+    // in an earlier split or end in a later one)
+    const int g0 = kbeg / group, ns = (kbeg + kspan - 1) / group - g0 + 1;
     for (int idx = tid; idx < BN * ns; idx += C::kThreads) {
       const int row = idx / ns;
       const int n = min(n0 + row, N - 1);
@@ -315,12 +317,14 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     mfmas(fa1, fb1);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kPost) {
-      // group ends with this step: acc += part * s[n, g]; part = 0
-      if (((ks + 1) * kBK) % group == 0) {
-        const int g = (ks * kBK) / group;
+      // a group (or this split's share of one) ends with this step:
+      // acc += part * s[n, g]; part = 0
+      if ((kbeg + (ks + 1) * kBK) % group == 0 || ks + 1 == ksteps) {
+        const int ns = (kbeg + kspan - 1) / group - kbeg / group + 1;
+        const int g = (kbeg + ks * kBK) / group - kbeg / group;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const float sj = Ssh[((wn * TN + j) * 16 + r16) * (kspan / group) + g];
+          const float sj = Ssh[((wn * TN + j) * 16 + r16) * ns + g];
 #pragma unroll
           for (int i = 0; i < TM; ++i) {
             acc[i][j] += part[i][j] * sj;
@@ -441,41 +445,74 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
   }
 }
 
-// Number of k splits for `tiles` output tiles: the largest of 8, 6, 4, 3, 2
-// that keeps tiles x splits <= 256 (one workgroup per CU), divides the 64-k
-// steps into runs of >= 4 and, for int8, keeps whole scale groups together.
+// int8 stages the scale rows of every group a split touches in kGemmScaleFloats
+// of LDS (128 rows): the fewest splits (dividing the 64-k steps) that keep a
+// split's groups within that; 0 = none does.  int4 needs no staging.
 template <int WBITS>
-static int choose_splits(int64_t tiles, int64_t K, int64_t G) {
+static int min_splits(int64_t K, int64_t G) {
+  if (WBITS == 4) return 1;
+  static_assert(GemmDefault::BN == 128 && GemmSmall::BN == 128, "scale staging sized for 128 rows");
   const int64_t ksteps = K / kBK;
-  for (int s : {8, 6, 4, 3, 2}) {
-    if (tiles * s > 256 || ksteps % s != 0 || ksteps / s < 4) continue;
-    if (WBITS == 8 && (K / s) % G != 0) continue;
-    return s;
+  for (int64_t s = 1; s <= ksteps && s <= 64; ++s) {
+    if (ksteps % s != 0) continue;
+    const int64_t span = K / s;
+    int64_t most = 0;   // groups the widest split touches
+    for (int64_t i = 0; i < s; ++i)
+      most = std::max(most, ((i + 1) * span - 1) / G - (i * span) / G + 1);
+    if (most <= kGemmScaleFloats / 128) return int(s);
   }
-  return 1;
+  return 0;
 }
 
+// Number of k splits for `tiles` output tiles: the largest of 8, 6, 4, 3, 2
+// that keeps tiles x splits <= 256 (one workgroup per CU) and divides the
+// 64-k steps into runs of >= 4, and at least `need`.
+static int choose_splits(int64_t tiles, int64_t K, int need) {
+  const int64_t ksteps = K / kBK;
+  for (int s : {8, 6, 4, 3, 2}) {
+    if (s < need || tiles * s > 256 || ksteps % s != 0 || ksteps / s < 4) continue;
+    return s;
+  }
+  return need;
+}
+
+template <class C, int WBITS, int SD, int OD>
+static int launch_gemm_split(const void* X, const void* W, const void* S, void* O, int64_t M,
+                             int64_t N, int64_t K, int64_t G, int splits, hipStream_t st) {
+  const size_t mn = size_t(M) * size_t(N);
+  const size_t ws_bytes = mn * sizeof(float) * size_t(splits);
+  void* ws = ws_bytes <= kSplitWsMax ? split_workspace(ws_bytes, st) : nullptr;
+  if (ws == nullptr) return LQ_ERR_SHAPE;
+  int rc = launch_gemm_cfg<C, WBITS, SD, LQ_F32>(X, W, S, ws, M, N, K, G, splits, st);
+  if (rc != LQ_OK) return rc;
+  hipLaunchKernelGGL((split_reduce_kernel<OD>), dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, st,
+                     static_cast<const float*>(ws), O, mn, splits);
+  return check_launch();
+}
+
+// LQ_ERR_SHAPE: no configuration applies (the caller takes another kernel).
 template <int WBITS, int SD, int OD>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int need = min_splits<WBITS>(K, G);
+  if (need == 0) return LQ_ERR_SHAPE;
   // 256-row tiles only when they alone give every CU (256) a tile; below that
   // (M <= 1024 at N = 4096) 128 x 128 tiles finish sooner, split over k when
   // they too leave CUs idle.
   const int64_t big_tiles = ((M + GemmDefault::BM - 1) / GemmDefault::BM) *
                             ((N + GemmDefault::BN - 1) / GemmDefault::BN);
-  if (big_tiles >= 256) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
+  if (big_tiles >= 256) {
+    if (need == 1) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
+    return launch_gemm_split<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, need, st);
+  }
   const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
                         ((N + GemmSmall::BN - 1) / GemmSmall::BN);
-  const int splits = choose_splits<WBITS>(tiles, K, G);
-  const size_t mn = size_t(M) * size_t(N);
-  const size_t ws_bytes = mn * sizeof(float) * size_t(splits);
-  void* ws = splits > 1 && ws_bytes <= kSplitWsMax ? split_workspace(ws_bytes, st) : nullptr;
-  if (ws == nullptr) return launch_gemm_cfg<GemmSmall, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
-  int rc = launch_gemm_cfg<GemmSmall, WBITS, SD, LQ_F32>(X, W, S, ws, M, N, K, G, splits, st);
-  if (rc != LQ_OK) return rc;
-  hipLaunchKernelGGL((split_reduce_kernel<OD>), dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, st,
-                     static_cast<const float*>(ws), O, mn, splits);
-  return check_launch();
+  const int splits = choose_splits(tiles, K, need);
+  if (splits > 1) {
+    const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD>(X, W, S, O, M, N, K, G, splits, st);
+    if (rc != LQ_ERR_SHAPE || need > 1) return rc;
+  }
+  return launch_gemm_cfg<GemmSmall, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
 }
 
 template <int WBITS>

@@ -217,11 +217,25 @@ def test_matvec_int4_partial_segment(M, N, K, G):
     (4, 128, 4096, 4096, 128, "f16"),    # 32 tiles, 8 splits
     (8, 128, 4096, 4096, 128, "f32"),
     (4, 300, 2048, 2048, 128, "f16"),    # 48 tiles, 4 splits
+    (8, 96, 4096, 11008, 128, "f16"),    # 86 scale groups > LDS: 4 splits, groups straddle splits
+    (8, 256, 640, 4096, 4096, "f32"),    # per-channel: splits shorter than the group
+    (8, 130, 384, 4096, 64, "f16"),      # 64 groups: fit without a forced split
 ])
 def test_matmul_prefill_split_k(wbits, M, N, K, G, od):
     X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=M * 7 + N + K)
     got = _matvec(wbits, X, W, S, N, K, G, od)
     _close(got, _oracle(wbits, X, W, S, G), fp32=False)
+
+
+def test_int8_prefill_forced_split_big_tiles():
+    """256-row tiles with more int8 scale groups (65) than LDS stages: K is
+    split in two although the tiles fill the CUs (oracle on a row subset)."""
+    M, N, K, G = 2048, 4096, 8320, 128
+    X, W, S = synth.matvec_case(8, M, N, K, G, 0.002, 0.02, seed=12)
+    got = _matvec(8, X, W, S, N, K, G, "f16")
+    rows = np.r_[0:32, 1000:1032, M - 32:M]
+    _close(got[rows], _oracle(8, X[rows], W, S, G))
+    assert np.isfinite(got.astype(np.float32)).all()
 
 
 def test_matmul_prefill_split_k_graph():
