@@ -1243,6 +1243,16 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
 // by the T weight tiles.  The group scale (G % 32 == 0) is applied in fp32.
 constexpr int kXChunkK = 256;
 constexpr int kXSlots = 3;
+// LDS of the ring (also the cross-wave sum) and of the scale rows: whatever
+// the ring leaves of 160 KB, at most kTScaleLds.
+constexpr int xl_ring_bytes(int wbits, int tiles) {
+  const int slot = 16 * tiles * kXChunkK * wbits / 8 + 64 * kXChunkK * 2;
+  return kXSlots * slot > 8 * 4 * tiles * 1024 ? kXSlots * slot : 8 * 4 * tiles * 1024;
+}
+constexpr int xl_scale_bytes(int wbits, int tiles) {
+  const int left = 160 * 1024 - xl_ring_bytes(wbits, tiles);
+  return (left > kTScaleLds ? kTScaleLds : left) & ~1023;
+}
 
 template <int WBITS, int TILES, int SD, int OD>
 __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
@@ -1262,11 +1272,12 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
   constexpr int kPerWaveMax = (kInstr + 7) / 8;
   static_assert(kWBytes % 1024 == 0, "whole weight DMA instructions");
   // the cross-wave sum reuses the ring (sized to hold it)
-  constexpr int kRingB = kXSlots * kSlotB > 8 * 4 * TILES * 1024 ? kXSlots * kSlotB
-                                                                  : 8 * 4 * TILES * 1024;
-  static_assert(kRingB + kTScaleLds / 2 <= 160 * 1024, "LDS budget");
+  constexpr int kRingB = xl_ring_bytes(WBITS, TILES);
+  static_assert(kRingB >= kXSlots * kSlotB, "ring holds the slots");
+  constexpr int kSclB = xl_scale_bytes(WBITS, TILES);
+  static_assert(kRingB + kSclB <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(16))) uint8_t ring[kRingB];
-  __shared__ __attribute__((aligned(16))) uint8_t sl[kTScaleLds / 2];
+  __shared__ __attribute__((aligned(16))) uint8_t sl[kSclB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1661,7 +1672,8 @@ static int gemv_tile_xl_count(int wbits, int64_t N, int64_t K, int64_t G, int sc
     if ((N + 16 * t - 1) / (16 * t) <= 256) { tiles = t; break; }
   // int4 rows are 128 bytes per chunk: whole 1 KB DMA instructions need T even
   if (wbits == 4 && (tiles & 1)) ++tiles;
-  while (tiles > 0 && 16 * tiles * (K / G) * scale_bytes > kTScaleLds / 2) tiles -= wbits == 4 ? 2 : 1;
+  while (tiles > 0 && 16 * tiles * (K / G) * scale_bytes > xl_scale_bytes(wbits, tiles))
+    tiles -= wbits == 4 ? 2 : 1;
   return tiles;
 }
 static bool gemv_tile_xl_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, int scale_bytes) {
@@ -1697,7 +1709,7 @@ static int launch_gemv_tile_xl(const void* X, const void* W, const void* S, void
 // within what compiles without spills (at most 4 for M <= 2, 2 for M <= 4).
 static bool gemv_diag_ok(int wbits, int64_t M, int64_t K, int64_t G) {
   const int64_t nseg = (K + 2047) / 2048;
-  return wbits == 4 && M <= 4 && G % 128 == 0 && K % 128 == 0 && K <= 16384 && K >= 128 &&
+  return wbits == 4 && M <= 4 && G % 128 == 0 && K % 128 == 0 && K <= 16384 && K >= 2048 &&
          (M <= 1 || (M <= 2 ? nseg <= 2 : nseg <= 1));
 }
 
@@ -1720,7 +1732,7 @@ template <int WBITS, int SD, int OD>
 static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void* O, int64_t M,
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
   if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
-    if (M >= 2 && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
+    if ((M >= 2 || WBITS == 8) && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
   if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
