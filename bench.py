@@ -287,6 +287,35 @@ def profile_case(name, launches=50):
     return 0
 
 
+SWEEP_M = (1, 2, 4, 8, 16, 32, 64, 96, 256, 1024)
+SWEEP_SHAPES = ((576, 576), (1536, 576), (576, 1536), (4096, 4096), (11008, 4096), (4096, 11008),
+                (14336, 4096))   # (N, K): SmolLM2-135M and LLaMA-7B-class linear layers
+
+
+def sweep():
+    """Microseconds per dequant-matmul launch (graph replays, weights rotated
+    through replicas larger than the Infinity Cache) over SWEEP_M x
+    SWEEP_SHAPES, int4 G = 32 / 128 and int8 G = 128 / per-channel; one
+    Markdown table on stdout."""
+    import torch
+    print("| bits | N | K | G | " + " | ".join(f"M={m}" for m in SWEEP_M) + " |")
+    print("|---|---|---|---|" + "---|" * len(SWEEP_M))
+    for wb in (4, 8):
+        for N, K in SWEEP_SHAPES:
+            for G in ((32, 128) if wb == 4 else (128, K)):
+                if K % G:
+                    continue
+                cells = []
+                for M in SWEEP_M:
+                    case = Case("matvec", wb, M, N, K, G, 0.001, 0.01, max_replicas=16)
+                    t, n = time_graph(case, 200, 20)
+                    cells.append(f"{t / n * 1e6:.1f}")
+                    del case
+                    torch.cuda.empty_cache()
+                print(f"| {wb} | {N} | {K} | {G} | " + " | ".join(cells) + " |", flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -296,6 +325,8 @@ def main():
     ap.add_argument("--only", default="", help="comma list of extra cases to run (default all)")
     ap.add_argument("--profile", default="", choices=["", "gemv", "gemv_m16", "gemm", "dequant", "w8a16", "copy"],
                     help="launch one case 50 times eagerly and exit (for rocprofv3 counter passes)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="time the dequant-matmul over a grid of M and linear-layer shapes, print a table")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -310,6 +341,8 @@ def main():
 
     if args.profile:
         return profile_case(args.profile)
+    if args.sweep:
+        return sweep()
 
     c3 = synth.CFG3
     log("case gemv_w4a16 M=1")
