@@ -1009,8 +1009,9 @@ __device__ __forceinline__ void dma16_buf(i32x4_t rsrc, uint32_t voff, const voi
 }
 
 // NSC = scale groups per wave k-eighth of a row (1, 2 or 4; 4 MFMA blocks);
-// TILES = 16-row weight tiles per workgroup (1 .. 4).
-template <int WBITS, int NSC, int TILES, int SD, int OD>
+// TILES = 16-row weight tiles per workgroup (1 .. 4); PART = the rows end in
+// a partial chunk (the masked path below; whole-chunk rows skip its cost).
+template <int WBITS, int NSC, int TILES, int SD, int OD, bool PART>
 __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
@@ -1037,16 +1038,27 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   const int q4 = lane >> 4;
   const int n0 = blockIdx.x * kRows;
   const int row_bytes = (WBITS == 4) ? (K >> 1) : K;
-  const int nchunks = row_bytes / kTChunkB;
+  // The last chunk may be partial (row_bytes % 512 != 0): its 16-byte
+  // positions past the row end take an out-of-range buffer offset and read
+  // zeros, the matching activations are zeroed in compute(), and the scale
+  // index is clamped to the row's last group.
+  const int nchunks = (row_bytes + kTChunkB - 1) / kTChunkB;
 
   // DMA: wave w copies rows 2 T w .. 2 T w + 2 T - 1 of each chunk, 2 rows
-  // per instruction.
+  // per instruction (PART: from a raw buffer over W).
   const uint8_t* dsrc[kDma];
+  const i32x4_t wrsrc = {int(uint32_t(reinterpret_cast<uint64_t>(W))),
+                         int(uint32_t(reinterpret_cast<uint64_t>(W) >> 32) & 0xFFFFu),
+                         int(uint32_t(N) * uint32_t(row_bytes)), 0x00020000};
+  uint32_t doff[kDma];   // byte offset of the lane's 16 bytes in chunk 0
+  int dpos[kDma];        // their position in the row's chunk
 #pragma unroll
   for (int i = 0; i < kDma; ++i) {
     const int row = wave * 2 * kDma + 2 * i + (lane >> 5);
     const int n = min(n0 + row, N - 1);
     const int c = (lane & 31) ^ (row & 15);
+    doff[i] = uint32_t(n) * uint32_t(row_bytes) + uint32_t(c * 16);
+    dpos[i] = c * 16;
     dsrc[i] = W + size_t(n) * row_bytes + c * 16;
   }
   // Workgroups start at different chunks (step c reads chunk (c + rot) mod
@@ -1057,8 +1069,14 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   auto dma_chunk = [&](int slot, int c) {
     const int ch = phys(c);
 #pragma unroll
-    for (int i = 0; i < kDma; ++i)
-      dma16(dsrc[i] + ch * kTChunkB, &wl[slot * kSlotB + (wave * 2 * kDma + 2 * i) * kTChunkB]);
+    for (int i = 0; i < kDma; ++i) {
+      void* dst = &wl[slot * kSlotB + (wave * 2 * kDma + 2 * i) * kTChunkB];
+      if constexpr (PART)
+        dma16_buf(wrsrc, ch * kTChunkB + dpos[i] < row_bytes ? doff[i] + uint32_t(ch * kTChunkB) : 0xFFFFFFF0u,
+                  dst);
+      else
+        dma16(dsrc[i] + ch * kTChunkB, dst);
+    }
   };
 
   // Lane (m = r16, q4) supplies activation row m, k = block * kSpan + q4 * kSpan / 4 + 0 ..
@@ -1073,9 +1091,11 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   auto load_batch = [&](Batch& bt, int c) {
     const int ch = phys(c);
     if (!x_lane) return;
+    const int k0 = ch * kChunkK + wave * kEighthK + q4 * (kSpan / 4);
 #pragma unroll
     for (int f = 0; f < kTBlocks; ++f) {
-      const half_t* px = xrow + ch * kChunkK + f * kSpan;
+      // past K (partial last chunk): load from the row start, zeroed in compute()
+      const half_t* px = !PART || k0 + f * kSpan < K ? xrow + ch * kChunkK + f * kSpan : X;
       if constexpr (sizeof(x_t) == 16) {
         bt.x[f] = gload_b128_cached(px);
       } else {
@@ -1128,7 +1148,8 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
       }
 #pragma unroll
       for (int sg = 0; sg < NSC; ++sg) {
-        const int g = (kbase + sg * kPerScale * kSpan) / group;
+        int g = (kbase + sg * kPerScale * kSpan) / group;
+        if constexpr (PART) g = min(g, num_scales - 1);
         const uint8_t* ps = sl + (size_t(row) * num_scales + g) * kSSize;
         if constexpr (SD == LQ_F32) sc[t][sg] = *reinterpret_cast<const float*>(ps);
         else if constexpr (SD == LQ_F16) sc[t][sg] = float(*reinterpret_cast<const half_t*>(ps));
@@ -1137,7 +1158,10 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
     }
     op_t xa[kTBlocks];
 #pragma unroll
-    for (int f = 0; f < kTBlocks; ++f) xa[f] = Mf::prep_x(bt.x[f]);
+    for (int f = 0; f < kTBlocks; ++f) {
+      xa[f] = Mf::prep_x(bt.x[f]);
+      if (PART && kbase + f * kSpan + q4 * (kSpan / 4) >= K) xa[f] = op_t{};
+    }
 #pragma unroll
     for (int sg = 0; sg < NSC; ++sg) {
       // bias chain of this scale group: one MFMA per block, shared by the tiles
@@ -1623,10 +1647,20 @@ static void launch_gemv_tile_t(const void* X, const void* W, const void* S, void
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const int tiles = gemv_tile_count(N, K, G, SD == LQ_F32 ? 4 : 2);
   const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
-#define LQ_TILE_LAUNCH(T_)                                                                     \
-  hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, SD, OD>), dim3(blocks), dim3(512), 0,   \
-                     st, static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,  \
-                     int(M), int(N), int(K), int(K / G), int(G))
+  const bool part = ((WBITS == 4 ? K / 2 : K) % kTChunkB) != 0;
+#define LQ_TILE_LAUNCH(T_)                                                                      \
+  do {                                                                                          \
+    if (part)                                                                                   \
+      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, SD, OD, true>), dim3(blocks),        \
+                         dim3(512), 0, st, static_cast<const half_t*>(X),                       \
+                         static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K),          \
+                         int(K / G), int(G));                                                   \
+    else                                                                                        \
+      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, SD, OD, false>), dim3(blocks),       \
+                         dim3(512), 0, st, static_cast<const half_t*>(X),                       \
+                         static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K),          \
+                         int(K / G), int(G));                                                   \
+  } while (0)
   switch (tiles) {
     case 1: LQ_TILE_LAUNCH(1); break;
     case 2: LQ_TILE_LAUNCH(2); break;
@@ -1649,7 +1683,8 @@ static int launch_gemv_tile(const void* X, const void* W, const void* S, void* O
   return check_launch();
 }
 
-// The LDS-ring tile kernel: 2 <= M <= 16, whole 512-byte chunks per row,
+// The LDS-ring tile kernel: 2 <= M <= 16 (int8 also M = 1), rows of at least
+// one 512-byte chunk (the last one may be partial), 16-byte multiples,
 // every wave k-eighth (128 k int4 / 64 k int8) either inside one group or
 // split into 2 or 4 whole groups of at least one MFMA block, and the scale
 // array a whole number of dwords whose rows fit the LDS scale area.
@@ -1659,7 +1694,8 @@ static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, 
   const int64_t eighth_k = kTBlocks * span;
   const bool groups_ok = G >= eighth_k ? G % eighth_k == 0
                                        : (G >= span && eighth_k % G == 0);
-  return M >= 1 && M <= 16 && row_bytes >= kTChunkB && row_bytes % kTChunkB == 0 && groups_ok &&
+  return M >= 1 && M <= 16 && row_bytes >= kTChunkB && row_bytes % 16 == 0 && groups_ok &&
+         N * row_bytes < (int64_t(1) << 31) &&
          (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_count(N, K, G, scale_bytes) > 0;
 }
 

@@ -207,6 +207,22 @@ def test_matvec_int4_partial_segment(M, N, K, G):
     _close(got, _oracle(4, X, W, S, G))
 
 
+# LDS-ring tile kernel with a partial last 512-byte row chunk (zeros past the
+# row end through out-of-range buffer offsets, activations zeroed past K).
+@pytest.mark.parametrize("wbits,M,N,K,G", [
+    (4, 4, 640, 11008, 128),     # 5504-byte rows: 10 chunks + 384 bytes
+    (4, 16, 300, 1536, 32),      # 768-byte rows
+    (4, 3, 257, 2080, 32),       # 1040-byte rows: 16 bytes in the last chunk
+    (8, 1, 1000, 11008, 128),    # int8 M = 1 takes this kernel too
+    (8, 8, 333, 1040, 16),
+    (8, 2, 130, 11008, 11008),   # per-channel
+])
+def test_matvec_tile_partial_chunk(wbits, M, N, K, G):
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=M + N + K + wbits)
+    got = _matvec(wbits, X, W, S, N, K, G, "f16")
+    _close(got, _oracle(wbits, X, W, S, G))
+
+
 # Split-K prefill (fewer 128 x 128 output tiles than CUs): k split 8, 6, 4
 # ways, fp32 partial slices reduced in order; odd M x N takes the scalar tail
 # of the reduction.  Cases run back to back, so the cached workspace grows.
