@@ -1768,7 +1768,9 @@ template <int WBITS, int SD, int OD>
 static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void* O, int64_t M,
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
   if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
-    if ((M >= 2 || WBITS == 8) && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
+    // int4 M = 1 keeps the segment / row kernels up to K = 8192 (faster there);
+    // longer rows stream better through the LDS ring.
+    if ((M >= 2 || WBITS == 8 || K > 8192) && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
   if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
