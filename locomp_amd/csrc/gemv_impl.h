@@ -1694,7 +1694,10 @@ static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, 
   const int64_t eighth_k = kTBlocks * span;
   const bool groups_ok = G >= eighth_k ? G % eighth_k == 0
                                        : (G >= span && eighth_k % G == 0);
+  // (a partial last chunk only behind >= 4 whole ones: on shorter rows the
+  // row / LDS kernels are faster)
   return M >= 1 && M <= 16 && row_bytes >= kTChunkB && row_bytes % 16 == 0 && groups_ok &&
+         (row_bytes % kTChunkB == 0 || row_bytes >= 4 * kTChunkB) &&
          N * row_bytes < (int64_t(1) << 31) &&
          (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_count(N, K, G, scale_bytes) > 0;
 }

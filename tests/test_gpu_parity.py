@@ -211,10 +211,10 @@ def test_matvec_int4_partial_segment(M, N, K, G):
 # row end through out-of-range buffer offsets, activations zeroed past K).
 @pytest.mark.parametrize("wbits,M,N,K,G", [
     (4, 4, 640, 11008, 128),     # 5504-byte rows: 10 chunks + 384 bytes
-    (4, 16, 300, 1536, 32),      # 768-byte rows
-    (4, 3, 257, 2080, 32),       # 1040-byte rows: 16 bytes in the last chunk
+    (4, 16, 300, 4128, 32),      # 2064-byte rows: 16 bytes in the last chunk
+    (4, 3, 257, 5120 + 96, 32),  # 2608-byte rows
     (8, 1, 1000, 11008, 128),    # int8 M = 1 takes this kernel too
-    (8, 8, 333, 1040, 16),
+    (8, 8, 333, 2064, 16),
     (8, 2, 130, 11008, 11008),   # per-channel
 ])
 def test_matvec_tile_partial_chunk(wbits, M, N, K, G):
