@@ -730,13 +730,14 @@ __global__ __launch_bounds__(256, 2) void gemv_diag_kernel(
 //     MFMA chain as its initial accumulator (negated), so the chain ends
 //     holding x . (q - 8) directly;
 //   * the diagonal is selected once per (row, segment), scaled, summed;
-//   * a last, partial segment (K % 2048 != 0, K % 128 == 0) takes buffer
+//   * PART (K % 2048 != 0, K % 128 == 0): the last segments take buffer
 //     offsets past the end for k >= K: activations, weights and scales read
-//     as zeros there (and cost no memory traffic), so those k add nothing.
+//     as zeros there (and cost no memory traffic), so those k add nothing;
+//     a separate instantiation, so whole-segment rows skip the selects.
 // lane offset past every buffer's end (sizes < 2^31 - 2^30 are checked on the host)
 constexpr int kSegOob = 0x40000000;
 
-template <int M_, int NSEG, int RW, int SD, int OD>
+template <int M_, int NSEG, int RW, int SD, int OD, bool PART>
 __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
@@ -767,7 +768,8 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 #pragma unroll
       for (int c = 0; c < NSEG; ++c)
         xv2[m][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-            rx, c * 2048 + tpos * 32 < K ? (m * K + c * 2048 + tpos * 32 + te * 8) * 2 : kSegOob, 0, 0));
+            rx, !PART || c * 2048 + tpos * 32 < K ? (m * K + c * 2048 + tpos * 32 + te * 8) * 2 : kSegOob,
+            0, 0));
   }
   // 2. scales
   uint32_t sv[RW][NSEG];
@@ -775,7 +777,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   for (int r = 0; r < RW; ++r)
 #pragma unroll
     for (int c = 0; c < NSEG; ++c) {
-      const bool kin = c * 2048 + pos * 32 < K;
+      const bool kin = !PART || c * 2048 + pos * 32 < K;
       const int g = (c * 2048 + pos * 32) / group;
       if constexpr (sizeof(stype) == 2)
         sv[r][c] = __builtin_amdgcn_raw_buffer_load_b16(rs, kin ? g * 2 : kSegOob, ((n0 + r) * num_scales) * 2, 0);
@@ -790,7 +792,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 #pragma unroll
     for (int c = 0; c < NSEG; ++c)
       wv[r][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-          rw, c * 2048 + pos * 32 < K ? c * 1024 + pos * 16 : kSegOob, (n0 + r) * half_k,
+          rw, !PART || c * 2048 + pos * 32 < K ? c * 1024 + pos * 16 : kSegOob, (n0 + r) * half_k,
           2 /* nontemporal */));
   __builtin_amdgcn_sched_barrier(0);
 
@@ -1596,9 +1598,14 @@ template <int M_, int NSEG, int RW, int SD, int OD>
 static int launch_gemv_seg_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                              int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const unsigned blocks = unsigned((N + 4 * RW - 1) / (4 * RW));
-  hipLaunchKernelGGL((gemv_seg_kernel<M_, NSEG, RW, SD, OD>), dim3(blocks), dim3(256), 0, st,
-                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
-                     int(N), int(K), int(K / G), int(G));
+  if (K % 2048)
+    hipLaunchKernelGGL((gemv_seg_kernel<M_, NSEG, RW, SD, OD, true>), dim3(blocks), dim3(256), 0, st,
+                       static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
+                       int(N), int(K), int(K / G), int(G));
+  else
+    hipLaunchKernelGGL((gemv_seg_kernel<M_, NSEG, RW, SD, OD, false>), dim3(blocks), dim3(256), 0, st,
+                       static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
+                       int(N), int(K), int(K / G), int(G));
   return check_launch();
 }
 
