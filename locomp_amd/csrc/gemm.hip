@@ -505,6 +505,12 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
     if (need == 1) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
     return launch_gemm_split<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, need, st);
   }
+  // Half the CUs or more with 256-row tiles: those tiles with k split in two
+  // beat twice as many 128-row tiles (M = 1024 at N = 4096: 62.7 -> 56.9 us).
+  if (big_tiles >= 128 && need <= 2 && (K / kBK) % 2 == 0 && K / kBK >= 8) {
+    const int rc = launch_gemm_split<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 2, st);
+    if (rc != LQ_ERR_SHAPE || need > 1) return rc;
+  }
   const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
                         ((N + GemmSmall::BN - 1) / GemmSmall::BN);
   const int splits = choose_splits(tiles, K, need);

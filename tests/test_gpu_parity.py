@@ -254,6 +254,18 @@ def test_int8_prefill_forced_split_big_tiles():
     assert np.isfinite(got.astype(np.float32)).all()
 
 
+@pytest.mark.parametrize("wbits", [4, 8])
+def test_prefill_big_tiles_split_two(wbits):
+    """128 <= 256-row tiles < 256 CUs: 256 x 128 tiles with k split in two
+    (oracle on a row subset)."""
+    M, N, K, G = 1024, 4096, 2048, 128
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=21 + wbits)
+    got = _matvec(wbits, X, W, S, N, K, G, "f16")
+    rows = np.r_[0:40, 500:540, M - 40:M]
+    _close(got[rows], _oracle(wbits, X[rows], W, S, G))
+    assert np.isfinite(got.astype(np.float32)).all()
+
+
 def test_matmul_prefill_split_k_graph():
     """Split-K GEMM + reduction captured in a graph: every replay (with eager
     work and synchronisations between them) matches the eager result."""
