@@ -1012,8 +1012,10 @@ __device__ __forceinline__ void dma16_buf(i32x4_t rsrc, uint32_t voff, const voi
 
 // NSC = scale groups per wave k-eighth of a row (1, 2 or 4; 4 MFMA blocks);
 // TILES = 16-row weight tiles per workgroup (1 .. 4); PART = the rows end in
-// a partial chunk (the masked path below; whole-chunk rows skip its cost).
-template <int WBITS, int NSC, int TILES, int SD, int OD, bool PART>
+// a partial chunk (the masked path below; whole-chunk rows skip its cost);
+// EPI = gate/up rows interleaved (2i, 2i + 1): store silu(gate) * up to
+// O [M, N / 2] instead of O [M, N].
+template <int WBITS, int NSC, int TILES, int SD, int OD, bool PART, bool EPI = false>
 __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
@@ -1248,7 +1250,15 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = q4 * 4 + r;
-      if (m < M && n < N) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+      if constexpr (EPI) {
+        // rows 2i (gate) and 2i + 1 (up) sit in lanes r16 and r16 ^ 1
+        const float up = __shfl_xor(v[r], 1, 64);
+        const float g = v[r];
+        if ((r16 & 1) == 0 && m < M && n < N)
+          store_f32<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up);
+      } else {
+        if (m < M && n < N) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+      }
     }
   }
 }
@@ -1649,7 +1659,7 @@ static int gemv_tile_count(int64_t N, int64_t K, int64_t G, int scale_bytes) {
   return tiles;
 }
 
-template <int WBITS, int NSC, int SD, int OD>
+template <int WBITS, int NSC, int SD, int OD, bool EPI = false>
 static void launch_gemv_tile_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const int tiles = gemv_tile_count(N, K, G, SD == LQ_F32 ? 4 : 2);
@@ -1658,12 +1668,12 @@ static void launch_gemv_tile_t(const void* X, const void* W, const void* S, void
 #define LQ_TILE_LAUNCH(T_)                                                                      \
   do {                                                                                          \
     if (part)                                                                                   \
-      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, SD, OD, true>), dim3(blocks),        \
+      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, SD, OD, true, EPI>), dim3(blocks),   \
                          dim3(512), 0, st, static_cast<const half_t*>(X),                       \
                          static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K),          \
                          int(K / G), int(G));                                                   \
     else                                                                                        \
-      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, SD, OD, false>), dim3(blocks),       \
+      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, SD, OD, false, EPI>), dim3(blocks),  \
                          dim3(512), 0, st, static_cast<const half_t*>(X),                       \
                          static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K),          \
                          int(K / G), int(G));                                                   \
@@ -1677,15 +1687,15 @@ static void launch_gemv_tile_t(const void* X, const void* W, const void* S, void
 #undef LQ_TILE_LAUNCH
 }
 
-template <int WBITS, int SD, int OD>
+template <int WBITS, int SD, int OD, bool EPI = false>
 static int launch_gemv_tile(const void* X, const void* W, const void* S, void* O, int64_t M,
                             int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const int64_t eighth_k = kTBlocks * TileMfma<WBITS>::kSpan;
   const int nsc = G >= eighth_k ? 1 : int(eighth_k / G);
   switch (nsc) {
-    case 1: launch_gemv_tile_t<WBITS, 1, SD, OD>(X, W, S, O, M, N, K, G, st); break;
-    case 2: launch_gemv_tile_t<WBITS, 2, SD, OD>(X, W, S, O, M, N, K, G, st); break;
-    default: launch_gemv_tile_t<WBITS, 4, SD, OD>(X, W, S, O, M, N, K, G, st); break;
+    case 1: launch_gemv_tile_t<WBITS, 1, SD, OD, EPI>(X, W, S, O, M, N, K, G, st); break;
+    case 2: launch_gemv_tile_t<WBITS, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st); break;
+    default: launch_gemv_tile_t<WBITS, 4, SD, OD, EPI>(X, W, S, O, M, N, K, G, st); break;
   }
   return check_launch();
 }
@@ -1820,6 +1830,16 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
 // (int4, M <= 2, G % 32 == 0).  Returns LQ_ERR_SHAPE when it does not apply.
 inline int launch_rows_silu(const void* X, const void* W, const void* S, void* O, int64_t M,
                             int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  // 2 <= M <= 16: the LDS-ring tile kernel with the same epilogue
+  if (M >= 2 && gemv_tile_ok(4, M, N, K, G, sd == LQ_F32 ? 4 : 2)) {
+#define LQ_TS(SD_, OD_) \
+    if (sd == SD_ && od == OD_) return launch_gemv_tile<4, SD_, OD_, true>(X, W, S, O, M, N, K, G, st)
+    LQ_TS(LQ_F16, LQ_F16);
+    LQ_TS(LQ_F16, LQ_F32);
+    LQ_TS(LQ_F32, LQ_F16);
+    LQ_TS(LQ_F32, LQ_F32);
+#undef LQ_TS
+  }
   if (!gemv_rows_ok(4, M, K, G)) return LQ_ERR_SHAPE;
 #define LQ_RS(SD_, OD_)                                                                       \
   if (sd == SD_ && od == OD_)                                                                 \

@@ -389,6 +389,9 @@ def _silu_mul_oracle(X, Wg, Sg, Wu, Su, G):
     (3, 64, 512, 64, "f16"),        # M > 2: generic kernel
     (1, 48, 256, 16, "f16"),        # G % 32 != 0: generic kernel
     (2, 40, 128, 32, "f32"),        # fp32 activations: generic kernel
+    (4, 1536, 2048, 32, "f16"),     # 2 <= M <= 16: LDS-ring tile kernel epilogue
+    (16, 520, 1024, 128, "f16"),    # ragged last tile (1040 rows)
+    (3, 300, 4128, 32, "f16"),      # tile kernel, partial last chunk
 ])
 def test_matvec_int4_silu_mul(policy, M, I, K, G, xd):
     dt = np.float16 if xd == "f16" else np.float32
