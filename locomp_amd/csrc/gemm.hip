@@ -151,45 +151,47 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   const uint8_t* wrow = W + size_t(bn) * row_bytes + (WBITS == 4 ? (kbeg >> 1) : kbeg) + b_part * Bg::kBytes;
   const stype* sp = static_cast<const stype*>(S) + size_t(bn) * num_scales;
   constexpr int kBWords = Bg::kBytes / 4;
-  // Packed weights: `bfar` receives the loads of step ks + 2 during step ks;
-  // at the end of the step (after its wait) they move to `bnear`, which the
-  // next step dequantises while its MFMAs run.
-  u32x4_t bfar, bnear;    // 16-byte loads (bnear also holds the 8-byte case)
-  u32x2_t bfar2;          // 8-byte loads
-  uint32_t sfar = 0, snear = 0;   // raw scale bits, converted when the tile is dequantised
-
-  auto load_b = [&](int k0) {
+  // Packed weights rotate through kBSets register sets, loaded kBSets steps
+  // ahead.  Three (int4): during step ks the loads of B(ks + 3) fill one,
+  // B(ks + 1) is dequantised from another, and the third holds B(ks + 2),
+  // which the step's middle wait covers.  Two (int8, whose post-scale
+  // accumulators leave no registers for a third): B(ks + 2) fills one and is
+  // waited for at the end of the step.  A set is never copied while its loads
+  // are in flight.
+  constexpr int kBSets = kPost ? 2 : 3;
+  struct BRegs {
+    u32x4_t b;      // 16-byte loads
+    u32x2_t b2;     // 8-byte loads
+    uint32_t s;     // raw scale bits, converted when the tile is dequantised
+  };
+  auto load_b = [&](BRegs& r, int k0) {
     const int kb = WBITS == 4 ? (k0 >> 1) : k0;          // byte offset of k0 in the row
-    if constexpr (kBWords == 4) bfar = gload_b128(wrow + kb);
-    else bfar2 = gload_b64(wrow + kb);
+    if constexpr (kBWords == 4) r.b = gload_b128(wrow + kb);
+    else r.b2 = gload_b64(wrow + kb);
     if constexpr (!kPost) {
       const stype* ps = sp + (kbeg + k0 + b_part * Bg::kSpanK) / group;
-      if constexpr (sizeof(stype) == 2) sfar = gload_u16(ps);
-      else sfar = gload_b32(ps);
+      if constexpr (sizeof(stype) == 2) r.s = gload_u16(ps);
+      else r.s = gload_b32(ps);
     }
   };
-  // WAIT_FAR(n): wait until at most n loads are outstanding; ties the `far`
-  // registers so their consumers (and the copy to `near`) stay below it.  A
-  // register written by an asm load must not be read (or copied) before this.
-#define WAIT_FAR(n)                                                                         \
-  do {                                                                                      \
-    if constexpr (kBWords == 4)                                                             \
-      __asm__ volatile("s_waitcnt vmcnt(%2)" : "+v"(bfar), "+v"(sfar) : "n"(n) : "memory"); \
-    else                                                                                    \
-      __asm__ volatile("s_waitcnt vmcnt(%2)" : "+v"(bfar2), "+v"(sfar) : "n"(n) : "memory");\
-  } while (0)
-#define FAR_TO_NEAR()                                                      \
-  do {                                                                     \
-    if constexpr (kBWords == 4) bnear = bfar;                              \
-    else bnear = u32x4_t{bfar2.x, bfar2.y, 0u, 0u};                        \
-    snear = sfar;                                                          \
-  } while (0)
-  auto store_b = [&](int stage) {
+  // Placed right after the wait that covers a set's loads: names its registers
+  // there, so no read of them is scheduled before the wait.
+  auto tie_b = [&](BRegs& r) {
+    if constexpr (kBWords == 4) __asm__ volatile("" : "+v"(r.b));
+    else __asm__ volatile("" : "+v"(r.b2));
+    if constexpr (!kPost) __asm__ volatile("" : "+v"(r.s));
+  };
+  auto store_b = [&](const BRegs& r, int stage) {
     float bs;
-    if constexpr (SD == LQ_F32) bs = __uint_as_float(snear);
-    else if constexpr (SD == LQ_F16) bs = float(__builtin_bit_cast(half_t, uint16_t(snear)));
-    else bs = bf16_to_f32(uint16_t(snear));
-    const uint32_t bq[4] = {bnear.x, bnear.y, bnear.z, bnear.w};   // first kBWords used
+    if constexpr (SD == LQ_F32) bs = __uint_as_float(r.s);
+    else if constexpr (SD == LQ_F16) bs = float(__builtin_bit_cast(half_t, uint16_t(r.s)));
+    else bs = bf16_to_f32(uint16_t(r.s));
+    uint32_t bq[4];   // first kBWords used
+    if constexpr (kBWords == 4) {
+      bq[0] = r.b.x; bq[1] = r.b.y; bq[2] = r.b.z; bq[3] = r.b.w;
+    } else {
+      bq[0] = r.b2.x; bq[1] = r.b2.y; bq[2] = 0u; bq[3] = 0u;
+    }
     const half_t hs = half_t(bs);
     const half2_t s2 = {hs, hs};
     half_t* dst = Bs[stage];
@@ -247,16 +249,19 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   }
 
   const int ksteps = kspan / kBK;
-  // prologue: A(0), A(1) by DMA; B(0) dequantised into LDS; B(1) in `near`
+  // prologue: A(0), A(1) by DMA; B(0) dequantised into LDS; B(1) (and B(2))
+  // in their register sets
+  BRegs r0, r1, r2;
   dma_a(0, 0);
   dma_a(1, min(1, ksteps - 1) * kBK);
-  load_b(0);
-  WAIT_FAR(0);
-  FAR_TO_NEAR();
-  store_b(0);
-  load_b(min(1, ksteps - 1) * kBK);
-  WAIT_FAR(0);
-  FAR_TO_NEAR();
+  load_b(r0, 0);
+  load_b(r1, min(1, ksteps - 1) * kBK);
+  if constexpr (kBSets == 3) load_b(r2, min(2, ksteps - 1) * kBK);
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  tie_b(r0);
+  tie_b(r1);
+  if constexpr (kBSets == 3) tie_b(r2);
+  store_b(r0, 0);
   __syncthreads();
 
   // MFMA operand fragments of one 32-k half step (kk): lane (r16, q4) holds
@@ -290,27 +295,30 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   h8 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
   read_frags(0, 0, 0, fa0, fb0);
   int a_stage = 0;
-  for (int ks = 0; ks < ksteps; ++ks) {
+  // rl: receives B(ks + kBSets); rs: holds B(ks + 1), dequantised now; rt
+  // (three sets): holds B(ks + 2), covered by this step's middle wait.
+  auto step = [&](int ks, BRegs& rl, const BRegs& rs, BRegs& rt) {
     const int b_stage = ks & 1;
     const int a_next = a_stage == 2 ? 0 : a_stage + 1;
     const int a_next2 = a_stage == 0 ? 2 : a_stage - 1;   // (a_stage + 2) % 3
-    // Issue B(ks + 2) then A(ks + 2) (branch-free: past the end they re-read
-    // the last step and land in buffers no one reads).  A stage (ks + 2) % 3
-    // and B stage (ks + 1) % 2 were last read in step ks - 1, before its
-    // middle barrier.
-    const int k2 = min(ks + 2, ksteps - 1) * kBK;
-    load_b(k2);
-    dma_a(a_next2, k2);
+    // Issue B(ks + kBSets) then A(ks + 2) (branch-free: past the end they
+    // re-read the last step and land in buffers no one reads).  A stage
+    // (ks + 2) % 3 and B stage (ks + 1) % 2 were last read in step ks - 1,
+    // before its middle barrier.
+    load_b(rl, min(ks + kBSets, ksteps - 1) * kBK);
+    dma_a(a_next2, min(ks + 2, ksteps - 1) * kBK);
     // The scheduling barriers keep each half's fragment reads ahead of the
     // other half's MFMAs (the scheduler would otherwise sink them to their use).
     read_frags(a_stage, b_stage, 1, fa1, fb1);
     __builtin_amdgcn_sched_barrier(0);
     mfmas(fa0, fb0);
-    store_b(b_stage ^ 1);                      // dequantise B(ks + 1)
+    store_b(rs, b_stage ^ 1);                  // dequantise B(ks + 1)
     __builtin_amdgcn_sched_barrier(0);
-    // A(ks + 1) landed (only this step's loads may remain) and B(ks + 1) is
-    // in LDS for every wave: the next step's first half can be read.
+    // Only this step's loads may remain: A(ks + 1) (and with three sets
+    // B(ks + 2)) landed, and after the barrier B(ks + 1) is in LDS for every
+    // wave: the next step's first half can be read.
     __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kBLoads + kADma) : "memory");
+    if constexpr (kBSets == 3) tie_b(rt);
     __syncthreads();
     read_frags(a_next, b_stage ^ 1, 0, fa0, fb0);
     __builtin_amdgcn_sched_barrier(0);
@@ -335,16 +343,31 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
         }
       }
     }
-    WAIT_FAR(kADma);                           // B(ks + 2) landed
-    FAR_TO_NEAR();
+    if constexpr (kBSets == 2) {
+      __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kADma) : "memory");   // B(ks + 2) landed
+      tie_b(rl);
+    }
     a_stage = a_next;
+  };
+  if constexpr (kBSets == 3) {
+    for (int ks = 0; ks < ksteps; ks += 3) {
+      step(ks, r0, r1, r2);
+      if (ks + 1 < ksteps) step(ks + 1, r1, r2, r0);
+      if (ks + 2 < ksteps) step(ks + 2, r2, r0, r1);
+    }
+  } else {
+    for (int ks = 0; ks < ksteps; ks += 2) {
+      step(ks, r0, r1, r2);
+      if (ks + 1 < ksteps) step(ks + 1, r1, r0, r2);
+    }
   }
 
-#undef WAIT_FAR
-#undef FAR_TO_NEAR
   // The last steps' A copies (clamped repeats) are still in flight: drain
   // them before the workgroup's LDS can be handed to another workgroup.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  tie_b(r0);
+  tie_b(r1);
+  if constexpr (kBSets == 3) tie_b(r2);
   // Epilogue: lane holds rows 4 * (lane / 16) + r, column lane % 16 of each tile.
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
