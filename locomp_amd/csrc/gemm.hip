@@ -14,9 +14,11 @@
 //     of one row per 8 lanes, XOR-swizzled chunk order chosen through the
 //     source addresses.  A 3-slot ring keeps steps ks + 1 and ks + 2 in flight.
 //   * Weights: the 128 x 32-byte (int4) or 128 x 64-byte (int8) tile of step
-//     ks + 2 is loaded into registers during step ks, dequantised during step
-//     ks + 1 to exact fp16 (q - 8) or q times the fp16 scale (one rounding) and written to an
-//     XOR-swizzled LDS tile (2 stages) that every wave reads as the B operand.
+//     ks + 3 (int4) / ks + 2 (int8) is loaded into registers during step ks,
+//     and each tile is dequantised during the step before its use to exact
+//     fp16 (q - 8) times the fp16 scale (one rounding; int8: the exact q) and
+//     written to an XOR-swizzled LDS tile (2 stages) that every wave reads as
+//     the B operand.
 //   * One barrier per step, in its middle: the MFMA operand fragments of each
 //     32-k half are read from LDS while the other half's MFMAs run (the next
 //     step's first half right after the barrier).  The loop's loads are
