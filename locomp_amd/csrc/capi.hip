@@ -23,6 +23,10 @@ int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, 
                     hipStream_t);
 int launch_silu_fast(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                      int64_t, int, int, hipStream_t);
+int launch_gemm_silu(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                     int64_t, int, int, hipStream_t);
+void* stream_workspace(int, size_t, hipStream_t);
+int launch_silu_pairs(const float*, void*, int64_t, int64_t, int, hipStream_t);
 int launch_generic_silu(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                         int64_t, int, int, int, hipStream_t);
 
@@ -180,8 +184,20 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
                     M * K_dim <= kMax32 && N * HALF_K <= kMax32 && N * NUM_SCALES <= kMax32 &&
                     scale_dtype != LQ_BF16 && out_dtype != LQ_BF16;
   if (fast) {
-    rc = launch_silu_fast(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
+    if (M > 64 && K_dim % 64 == 0)   // prefill: the MFMA GEMM with the epilogue
+      rc = launch_gemm_silu(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
+    else
+      rc = launch_silu_fast(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
     if (rc != LQ_ERR_SHAPE) return rc;
+    // No fused kernel for this shape: the fast matvec into an fp32 staging
+    // buffer (slot 1 of the stream's workspace), then the pairwise epilogue.
+    void* P = stream_workspace(1, size_t(M) * size_t(N) * sizeof(float), st);
+    if (P != nullptr) {
+      rc = matmul_dispatch<4>(X, W, scales, P, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
+                              LQ_F32, st);
+      if (rc != LQ_OK) return rc;
+      return launch_silu_pairs(static_cast<const float*>(P), O, M, N, out_dtype, st);
+    }
   }
   return launch_generic_silu(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
                              out_dtype, st);

@@ -85,7 +85,9 @@ constexpr int kAStages = 3;   // activation ring: steps ks, ks + 1, ks + 2
 constexpr int kGemmScaleFloats = 8192;   // int8 post-scale: BN x (K / G) fp32 scales
 constexpr int kBStages = 2;
 
-template <class C, int WBITS, int SD, int OD>
+// EPI: gate/up rows interleaved (2i, 2i + 1); store silu(gate) * up to
+// O [M, N / 2] (columns n and n + 1 sit in lanes r16 and r16 ^ 1).
+template <class C, int WBITS, int SD, int OD, bool EPI = false>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int tiles_m, int tiles_n,
@@ -376,11 +378,17 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = m0 + wrow0 + i * 16 + q4 * 4 + r;
-      if (m >= M) continue;
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int n = n0 + (wn * TN + j) * 16 + r16;
-        if (n < N) store_f32<OD>(O, obase + size_t(m) * N + n, acc[i][j][r]);
+        if constexpr (EPI) {
+          const float g = acc[i][j][r];
+          const float up = __shfl_xor(g, 1, 64);
+          if ((r16 & 1) == 0 && m < M && n < N)
+            store_f32<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up);
+        } else {
+          if (m < M && n < N) store_f32<OD>(O, obase + size_t(m) * N + n, acc[i][j][r]);
+        }
       }
     }
   }
@@ -391,12 +399,12 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #endif
 typedef GemmCfg<LQ_GEMM_CFG> GemmDefault;   // default: 256 x 128 tile, 8 waves of 32 x 128
 
-template <class C, int WBITS, int SD, int OD>
+template <class C, int WBITS, int SD, int OD, bool EPI = false>
 static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O, int64_t M,
                            int64_t N, int64_t K, int64_t G, int splits, hipStream_t st) {
   const int tiles_m = int((M + C::BM - 1) / C::BM);
   const int tiles_n = int((N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm_w4_kernel<C, WBITS, SD, OD>), dim3(unsigned(tiles_m * tiles_n), unsigned(splits)),
+  hipLaunchKernelGGL((gemm_w4_kernel<C, WBITS, SD, OD, EPI>), dim3(unsigned(tiles_m * tiles_n), unsigned(splits)),
                      dim3(C::kThreads), 0, st, static_cast<const half_t*>(X),
                      static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K), int(K / G),
                      int(G), tiles_m, tiles_n, int(K / splits));
@@ -413,24 +421,26 @@ typedef GemmCfg<4, 2, 2, 4> GemmSmall;     // 128 x 128 tile, 8 waves of 32 x 64
 // buffer is never freed while the process runs (a captured graph may still
 // name it), and a call on a capturing stream that would need a larger one
 // runs unsplit instead.  Calls on one stream are ordered; different streams
-// have different workspaces.
+// have different workspaces.  Slot 0 holds split-K partials, slot 1 the
+// staged matvec of the SiLU * mul fallback (which may itself split K).
 constexpr size_t kSplitWsMax = size_t(256) << 20;
 
 struct SplitWs {
   int dev;
   hipStream_t st;
+  int slot;
   void* p;
   size_t bytes;
 };
 static std::mutex g_ws_mu;
 static std::vector<SplitWs> g_ws;
 
-static void* split_workspace(size_t bytes, hipStream_t st) {
+void* stream_workspace(int slot, size_t bytes, hipStream_t st) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  if (bytes > kSplitWsMax || hipGetDevice(&dev) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lock(g_ws_mu);
   for (SplitWs& w : g_ws)
-    if (w.dev == dev && w.st == st && w.bytes >= bytes) return w.p;
+    if (w.dev == dev && w.st == st && w.slot == slot && w.bytes >= bytes) return w.p;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
   size_t sz = size_t(1) << 20;
@@ -441,14 +451,15 @@ static void* split_workspace(size_t bytes, hipStream_t st) {
     return nullptr;
   }
   for (SplitWs& w : g_ws)
-    if (w.dev == dev && w.st == st) {   // grown: the old buffer stays allocated
+    if (w.dev == dev && w.st == st && w.slot == slot) {   // grown: the old buffer stays allocated
       w.p = p;
       w.bytes = sz;
       return p;
     }
-  g_ws.push_back(SplitWs{dev, st, p, sz});
+  g_ws.push_back(SplitWs{dev, st, slot, p, sz});
   return p;
 }
+static void* split_workspace(size_t bytes, hipStream_t st) { return stream_workspace(0, bytes, st); }
 
 template <int OD>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ P,
@@ -489,6 +500,26 @@ static int min_splits(int64_t K, int64_t G) {
   return 0;
 }
 
+// EPI form of the reduction: O [M, N / 2] = silu(sum of column 2i) * sum of
+// column 2i + 1.
+template <int OD>
+__global__ __launch_bounds__(256) void split_reduce_silu_kernel(const float* __restrict__ P,
+                                                                void* __restrict__ O, int64_t M,
+                                                                int64_t N, int splits) {
+  const int64_t half = N / 2;
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= M * half) return;
+  const int64_t m = e / half, i = e - m * half;
+  const size_t mn = size_t(M) * size_t(N);
+  const size_t at = size_t(m) * N + 2 * i;
+  float g = P[at], u = P[at + 1];
+  for (int s = 1; s < splits; ++s) {
+    g += P[size_t(s) * mn + at];
+    u += P[size_t(s) * mn + at + 1];
+  }
+  store_f32<OD>(O, size_t(e), g / (1.0f + expf(-g)) * u);
+}
+
 // Number of k splits for `tiles` output tiles: the largest of 8, 6, 4, 3, 2
 // that keeps tiles x splits <= 256 (one workgroup per CU) and divides the
 // 64-k steps into runs of >= 4, and at least `need`.
@@ -501,7 +532,7 @@ static int choose_splits(int64_t tiles, int64_t K, int need) {
   return need;
 }
 
-template <class C, int WBITS, int SD, int OD>
+template <class C, int WBITS, int SD, int OD, bool EPI = false>
 static int launch_gemm_split(const void* X, const void* W, const void* S, void* O, int64_t M,
                              int64_t N, int64_t K, int64_t G, int splits, hipStream_t st) {
   const size_t mn = size_t(M) * size_t(N);
@@ -510,13 +541,17 @@ static int launch_gemm_split(const void* X, const void* W, const void* S, void* 
   if (ws == nullptr) return LQ_ERR_SHAPE;
   int rc = launch_gemm_cfg<C, WBITS, SD, LQ_F32>(X, W, S, ws, M, N, K, G, splits, st);
   if (rc != LQ_OK) return rc;
-  hipLaunchKernelGGL((split_reduce_kernel<OD>), dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, st,
-                     static_cast<const float*>(ws), O, mn, splits);
+  if constexpr (EPI)
+    hipLaunchKernelGGL((split_reduce_silu_kernel<OD>), dim3(unsigned((mn / 2 + 255) / 256)), dim3(256),
+                       0, st, static_cast<const float*>(ws), O, M, N, splits);
+  else
+    hipLaunchKernelGGL((split_reduce_kernel<OD>), dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, st,
+                       static_cast<const float*>(ws), O, mn, splits);
   return check_launch();
 }
 
 // LQ_ERR_SHAPE: no configuration applies (the caller takes another kernel).
-template <int WBITS, int SD, int OD>
+template <int WBITS, int SD, int OD, bool EPI = false>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const int need = min_splits<WBITS>(K, G);
@@ -527,23 +562,23 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
   const int64_t big_tiles = ((M + GemmDefault::BM - 1) / GemmDefault::BM) *
                             ((N + GemmDefault::BN - 1) / GemmDefault::BN);
   if (big_tiles >= 256) {
-    if (need == 1) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
-    return launch_gemm_split<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, need, st);
+    if (need == 1) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 1, st);
+    return launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, need, st);
   }
   // Half the CUs or more with 256-row tiles: those tiles with k split in two
   // beat twice as many 128-row tiles (M = 1024 at N = 4096: 62.7 -> 56.9 us).
   if (big_tiles >= 128 && need <= 2 && (K / kBK) % 2 == 0 && K / kBK >= 8) {
-    const int rc = launch_gemm_split<GemmDefault, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 2, st);
+    const int rc = launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 2, st);
     if (rc != LQ_ERR_SHAPE || need > 1) return rc;
   }
   const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
                         ((N + GemmSmall::BN - 1) / GemmSmall::BN);
   const int splits = choose_splits(tiles, K, need);
   if (splits > 1) {
-    const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD>(X, W, S, O, M, N, K, G, splits, st);
+    const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, splits, st);
     if (rc != LQ_ERR_SHAPE || need > 1) return rc;
   }
-  return launch_gemm_cfg<GemmSmall, WBITS, SD, OD>(X, W, S, O, M, N, K, G, 1, st);
+  return launch_gemm_cfg<GemmSmall, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 1, st);
 }
 
 template <int WBITS>
@@ -562,6 +597,32 @@ int launch_gemm(const void* X, const void* W, const void* S, void* O, int64_t M,
   LQ_GM(LQ_BF16, LQ_BF16);
 #undef LQ_GM
   return LQ_ERR_DTYPE;
+}
+
+// O [M, N / 2] = silu(P[:, 2i]) * P[:, 2i + 1] for an fp32 matvec result P.
+int launch_silu_pairs(const float* P, void* O, int64_t M, int64_t N, int od, hipStream_t st) {
+  const unsigned blocks = unsigned((M * (N / 2) + 255) / 256);
+  if (od == LQ_F16)
+    hipLaunchKernelGGL((split_reduce_silu_kernel<LQ_F16>), dim3(blocks), dim3(256), 0, st, P, O, M, N, 1);
+  else if (od == LQ_F32)
+    hipLaunchKernelGGL((split_reduce_silu_kernel<LQ_F32>), dim3(blocks), dim3(256), 0, st, P, O, M, N, 1);
+  else
+    hipLaunchKernelGGL((split_reduce_silu_kernel<LQ_BF16>), dim3(blocks), dim3(256), 0, st, P, O, M, N, 1);
+  return check_launch();
+}
+
+// Gate|up prefill with the SiLU * mul epilogue (int4, N = 2 I interleaved rows).
+int launch_gemm_silu(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                     int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  if (G % 32 != 0) return LQ_ERR_SHAPE;
+#define LQ_GS(SD_, OD_) \
+  if (sd == SD_ && od == OD_) return launch_gemm_t<4, SD_, OD_, true>(X, W, S, O, M, N, K, G, st)
+  LQ_GS(LQ_F16, LQ_F16);
+  LQ_GS(LQ_F16, LQ_F32);
+  LQ_GS(LQ_F32, LQ_F16);
+  LQ_GS(LQ_F32, LQ_F32);
+#undef LQ_GS
+  return LQ_ERR_SHAPE;
 }
 
 template int launch_gemm<4>(const void*, const void*, const void*, void*, int64_t, int64_t,

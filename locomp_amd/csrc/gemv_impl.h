@@ -1290,7 +1290,8 @@ constexpr int xl_scale_bytes(int wbits, int tiles) {
   return (left > kTScaleLds ? kTScaleLds : left) & ~1023;
 }
 
-template <int WBITS, int TILES, int SD, int OD>
+// EPI: gate/up rows interleaved; store silu(gate) * up to O [M, N / 2].
+template <int WBITS, int TILES, int SD, int OD, bool EPI = false>
 __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
@@ -1485,7 +1486,14 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = mt * 16 + q4 * 4 + r;
-      if (m < M && n < N) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+      if constexpr (EPI) {
+        const float g = v[r];
+        const float up = __shfl_xor(g, 1, 64);
+        if ((r16 & 1) == 0 && m < M && n < N)
+          store_f32<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up);
+      } else {
+        if (m < M && n < N) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+      }
     }
   }
 }
@@ -1736,13 +1744,13 @@ static bool gemv_tile_xl_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t 
   return M > 16 && M <= 64 && K % kXChunkK == 0 && G % 32 == 0 &&
          (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_xl_count(wbits, N, K, G, scale_bytes) > 0;
 }
-template <int WBITS, int SD, int OD>
+template <int WBITS, int SD, int OD, bool EPI = false>
 static int launch_gemv_tile_xl(const void* X, const void* W, const void* S, void* O, int64_t M,
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const int tiles = gemv_tile_xl_count(WBITS, N, K, G, SD == LQ_F32 ? 4 : 2);
   const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
 #define LQ_TX(T_)                                                                              \
-  hipLaunchKernelGGL((gemv_tile_xl_kernel<WBITS, T_, SD, OD>), dim3(blocks), dim3(512), 0, st, \
+  hipLaunchKernelGGL((gemv_tile_xl_kernel<WBITS, T_, SD, OD, EPI>), dim3(blocks), dim3(512), 0, st, \
                      static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,     \
                      int(M), int(N), int(K), int(K / G), int(G))
   if constexpr (WBITS == 8) {
@@ -1830,6 +1838,16 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
 // (int4, M <= 2, G % 32 == 0).  Returns LQ_ERR_SHAPE when it does not apply.
 inline int launch_rows_silu(const void* X, const void* W, const void* S, void* O, int64_t M,
                             int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  // 16 < M <= 64: the activation-in-LDS kernel with the same epilogue
+  if (gemv_tile_xl_ok(4, M, N, K, G, sd == LQ_F32 ? 4 : 2)) {
+#define LQ_XS(SD_, OD_) \
+    if (sd == SD_ && od == OD_) return launch_gemv_tile_xl<4, SD_, OD_, true>(X, W, S, O, M, N, K, G, st)
+    LQ_XS(LQ_F16, LQ_F16);
+    LQ_XS(LQ_F16, LQ_F32);
+    LQ_XS(LQ_F32, LQ_F16);
+    LQ_XS(LQ_F32, LQ_F32);
+#undef LQ_XS
+  }
   // 2 <= M <= 16: the LDS-ring tile kernel with the same epilogue
   if (M >= 2 && gemv_tile_ok(4, M, N, K, G, sd == LQ_F32 ? 4 : 2)) {
 #define LQ_TS(SD_, OD_) \
