@@ -1797,8 +1797,11 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
   if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
     // int4 M = 1 keeps the segment / row kernels up to K = 8192 (faster there);
-    // longer rows stream better through the LDS ring.
-    if ((M >= 2 || WBITS == 8 || K > 8192) && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
+    // longer rows stream better through the LDS ring.  int4 M = 2 also takes
+    // the segment kernel for K >= 4096 and N <= 8192 (4096 x 4096: 4.9 against
+    // 6.1 us; at N = 11008 or K = 2048 the ring wins).
+    const bool seg2 = WBITS == 4 && M == 2 && K >= 4096 && N <= 8192 && gemv_seg_ok(WBITS, M, N, K, G);
+    if (!seg2 && (M >= 2 || WBITS == 8 || K > 8192) && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
   if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {

@@ -200,6 +200,8 @@ def test_int8_prefill_large():
     (3, 96, 6144, 256),
     (4, 257, 14336, 128),     # 7 segments -> 8
     (1, 100, 3200, 640),
+    (2, 4096, 4096, 128),     # M = 2 on the segment kernel (whole segments)
+    (2, 1000, 5120, 128),     # M = 2, 2.5 segments -> 4
 ])
 def test_matvec_int4_partial_segment(M, N, K, G):
     X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K)
