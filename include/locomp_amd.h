@@ -17,7 +17,10 @@
  * rows M, element dtypes, a HIP stream).
  *
  * Conventions
- *   - All pointers are device pointers; the library allocates nothing.
+ *   - All pointers are device pointers.  The library allocates only a
+ *     grow-only fp32 workspace per (device, stream), on the first prefill
+ *     that splits K and on the first SiLU * mul call without a fused kernel;
+ *     it is held until the process ends.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
  *     is asynchronous: the caller synchronises.
  *   - Return value: 0 on success; a negative LQ_ERR_* for invalid arguments
