@@ -10,7 +10,8 @@
 //   38:   s = amax > 0 ? amax / 7 (or / 127) : 1        q = round(w / s)
 //   52:   s = max(amax, 1e-10f) / 7                      q = round(w / (s + 1e-10f))
 //   int4: q = clip(q + 8, 0, 15), byte j = q[2j] | q[2j+1] << 4;  int8: clip(q, -128, 127)
-// Division is IEEE correctly rounded (HIP's default for float '/'); rounding
+// Division is IEEE correctly rounded (HIP's float '/', or the shared-
+// reciprocal form below, which gives the same result); rounding
 // is half-to-even (v_rndne_f32 = np.round).
 //
 // Layout: lane = 8 consecutive weights of one row (two 16-byte loads for
@@ -65,6 +66,16 @@ __device__ __forceinline__ void group_scale(float amax, float& s, float& div) {
   }
 }
 
+// w / d correctly rounded with y = RN(1 / d) shared by the lane's 8 weights
+// (Markstein's correction: q0 = RN(w y), r = w - q0 d exactly by an fma,
+// RN(q0 + r y) = RN(w / d)); one correctly rounded division per lane
+// instead of eight.  The caller keeps d and 1 / d normal and finite.
+__device__ __forceinline__ float div_shared(float w, float d, float y) {
+  const float q0 = w * y;
+  const float r = __builtin_fmaf(-q0, d, w);
+  return __builtin_fmaf(r, y, q0);
+}
+
 template <int MODE, int DT, int LPG>   // LPG = lanes per group = G / 8
 __global__ __launch_bounds__(256) void quantize_lane8_kernel(
     const void* __restrict__ W, uint8_t* __restrict__ Q, float* __restrict__ S, int N, int K,
@@ -87,11 +98,22 @@ __global__ __launch_bounds__(256) void quantize_lane8_kernel(
   for (int d = 1; d < LPG; d <<= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
   float s, div;
   group_scale<MODE>(amax, s, div);
+  // shared reciprocal where d and 1 / d are comfortably normal, else divide
+  const bool shared = div > 1e-30f && div < 1e30f;
+  float qv[8];
+  if (shared) {
+    const float y = 1.0f / div;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qv[i] = div_shared(w[i], div, y);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qv[i] = w[i] / div;
+  }
   if constexpr (MODE == kQ8Ref38) {
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float q = fminf(fmaxf(__builtin_rintf(w[i] / div), -128.0f), 127.0f);
+      const float q = fminf(fmaxf(__builtin_rintf(qv[i]), -128.0f), 127.0f);
       const uint32_t b = uint32_t(int(q)) & 0xFFu;
       if (i < 4) lo |= b << (8 * i);
       else hi |= b << (8 * (i - 4));
@@ -101,7 +123,7 @@ __global__ __launch_bounds__(256) void quantize_lane8_kernel(
     uint32_t p = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float q = fminf(fmaxf(__builtin_rintf(w[i] / div) + 8.0f, 0.0f), 15.0f);
+      const float q = fminf(fmaxf(__builtin_rintf(qv[i]) + 8.0f, 0.0f), 15.0f);
       p |= uint32_t(q) << (4 * i);
     }
     if (live) *reinterpret_cast<uint32_t*>(Q + row * (K >> 1) + size_t(k8) * 4) = p;

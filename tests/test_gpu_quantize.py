@@ -116,3 +116,29 @@ def test_quantize_then_dequantize_round_trip():
     d = O.numpy().reshape(N, K)
     s = np.repeat(S.numpy(), G, axis=1)
     assert np.all(np.abs(w - d) <= s * 0.5 + 1e-7 * np.abs(w))
+
+
+@pytest.mark.parametrize("fn,rf,top", [("quantize_int4", "quantize_int4", 7.0),
+                                      ("quantize_int4_ref", "quantize_int4_ref", 7.0),
+                                      ("quantize_int8", "quantize_int8", 127.0)])
+def test_quantize_rounding_ties(fn, rf, top):
+    """Quotients w / s within a few ulps of half-integers, over scales from
+    1e-20 to 1e20: the quantizer's division (one shared reciprocal per lane
+    plus an fma correction) must round exactly as NumPy's float32 division
+    before np.round, on every tie-adjacent value."""
+    rng = np.random.default_rng(99)
+    N, G = 8192, 8
+    K = 8 * G
+    amax = (10.0 ** rng.uniform(-20, 20, size=(N, K // G))).astype(np.float32)
+    s = (amax / np.float32(top)).astype(np.float32)
+    half = rng.integers(-int(top), int(top), size=(N, K)).astype(np.float32) + np.float32(0.5)
+    ulps = rng.integers(-3, 4, size=(N, K)).astype(np.float32)
+    sr = np.repeat(s, G, axis=1)
+    w = (half * sr).astype(np.float32)
+    w = (w + ulps * np.spacing(w)).astype(np.float32)
+    w = np.clip(w, -np.repeat(amax, G, axis=1), np.repeat(amax, G, axis=1)).astype(np.float32)
+    w[:, ::G] = np.repeat(amax, 1, axis=1) * np.where(rng.random((N, K // G)) < 0.5, 1, -1).astype(np.float32)
+    q, sc = getattr(lq, fn)(w, G)
+    qr, scr = getattr(ref, rf)(w, G)
+    _eq(sc, scr)
+    _eq(q, qr)
