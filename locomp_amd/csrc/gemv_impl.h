@@ -1808,6 +1808,12 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
     if (gemv_tile_xl_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile_xl<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
+  if constexpr (WBITS == 4 && (SD == LQ_BF16 || OD == LQ_BF16)) {
+    // bf16 scales or output at M = 1: the segment kernel (instantiated for
+    // M = 1 only; other M take the LDS / skinny kernels)
+    if (M == 1 && gemv_seg_ok(WBITS, M, N, K, G))
+      return launch_gemv_seg_m<1, SD, OD>(X, W, S, O, M, N, K, G, st);
+  }
   if constexpr (WBITS == 4 && SD != LQ_BF16 && OD != LQ_BF16) {
     if (gemv_seg_ok(WBITS, M, N, K, G)) {
       if (M == 1) return launch_gemv_seg_m<1, SD, OD>(X, W, S, O, M, N, K, G, st);

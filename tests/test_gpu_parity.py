@@ -225,6 +225,33 @@ def test_matvec_tile_partial_chunk(wbits, M, N, K, G):
     _close(got, _oracle(wbits, X, W, S, G))
 
 
+@pytest.mark.parametrize("sd,od", [("bf16", "f16"), ("f16", "bf16"), ("bf16", "bf16"), ("f32", "bf16")])
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 4096), (1, 300, 6144), (3, 200, 2048)])
+def test_matvec_int4_bf16_scales_or_output(sd, od, M, N, K):
+    """bf16 scales and/or bf16 outputs (M = 1: the segment kernel, partial
+    segments included; M = 3: the LDS / skinny kernels).  The oracle uses
+    the bf16-rounded scales; bf16 outputs are compared after widening."""
+    G = 128
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K)
+    S = S.astype(np.float32)
+    if sd == "bf16":
+        S_used = ref.bf16_bits_to_f32(ref.f32_to_bf16_bits(S)).reshape(S.shape)
+        Sg = _up(S, "bf16")
+    elif sd == "f16":
+        S_used = S.astype(np.float16).astype(np.float32)
+        Sg = _up(S.astype(np.float16))
+    else:
+        S_used = S
+        Sg = _up(S)
+    Og = lq.empty((M, N), _dtype(od))
+    lq.dequant_matvec_int4[(N,), (128,)](_up(X), _up(W), Sg, Og, K, K // 2, K // G, G)
+    got = Og.numpy()
+    got = ref.bf16_bits_to_f32(got).reshape(M, N) if od == "bf16" else got.astype(np.float32)
+    want = ref.fast_numpy_matvec_int4(X, W, S_used, G)
+    tol = 1e-2 if od != "bf16" else 2e-2   # bf16 output: 8-bit mantissa (rel 2^-9)
+    np.testing.assert_allclose(got, want, rtol=tol, atol=1e-2)
+
+
 # Split-K prefill (fewer 128 x 128 output tiles than CUs): k split 8, 6, 4
 # ways, fp32 partial slices reduced in order; odd M x N takes the scalar tail
 # of the reduction.  Cases run back to back, so the cached workspace grows.
