@@ -1795,7 +1795,10 @@ static int launch_skinny_mt(const void* X, const void* W, const void* S, void* O
 template <int WBITS, int SD, int OD>
 static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void* O, int64_t M,
                                int64_t N, int64_t K, int64_t G, hipStream_t st) {
-  if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
+  // the LDS-ring tile kernel also serves bf16 scales / outputs (not mixed
+  // with fp32, to bound the instantiations)
+  constexpr bool kTileDt = !(SD == LQ_F32 && OD == LQ_BF16) && !(SD == LQ_BF16 && OD == LQ_F32);
+  if constexpr (kTileDt) {
     // int4 M = 1 keeps the segment / row kernels up to K = 8192 (faster there);
     // longer rows stream better through the LDS ring.  int4 M = 2 also takes
     // the segment kernel for K >= 4096 and N <= 8192 (4096 x 4096: 4.9 against
