@@ -1807,7 +1807,7 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
     if (!seg2 && (M >= 2 || WBITS == 8 || K > 8192) && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
-  if constexpr (SD != LQ_BF16 && OD != LQ_BF16) {
+  if constexpr (kTileDt) {
     if (gemv_tile_xl_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile_xl<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }

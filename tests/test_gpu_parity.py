@@ -227,7 +227,7 @@ def test_matvec_tile_partial_chunk(wbits, M, N, K, G):
 
 @pytest.mark.parametrize("sd,od", [("bf16", "f16"), ("f16", "bf16"), ("bf16", "bf16"), ("f32", "bf16")])
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 4096), (1, 300, 6144), (3, 200, 2048), (4, 1000, 4096),
-                                   (16, 300, 2048), (1, 200, 11008)])
+                                   (16, 300, 2048), (1, 200, 11008), (40, 300, 2048)])
 def test_matvec_int4_bf16_scales_or_output(sd, od, M, N, K):
     """bf16 scales and/or bf16 outputs (M = 1: the segment kernel, partial
     segments included, or the LDS-ring tile kernel for K > 8192; M >= 2: the
