@@ -11,11 +11,15 @@ Method:
   * inputs are uploaded once and resident in HBM before timing;
   * each configuration cycles through R weight/scale replicas whose total
     exceeds MI355X's 256 MB Infinity Cache, so weights stream from HBM;
-  * launches are captured in a HIP graph (torch.cuda.CUDAGraph over the
-    library's launches on the capture stream) and replayed, so host launch
-    cost does not gap the GPU; HIP events on that stream bracket the replays;
-  * roofline.achieved = algorithmic bytes (or FLOPs) per launch / average
-    launch duration over the timed replays.
+  * a trial is one replay of a HIP graph holding `--steps` launches
+    (torch.cuda.CUDAGraph over the library's launches on the capture stream),
+    so host launch cost does not gap the GPU; HIP events on that stream
+    bracket each of 21 trials, enqueued back to back; a launch's time is the
+    median trial / `--steps`;
+  * roofline.achieved = algorithmic bytes (or FLOPs) per launch / that
+    median; roofline.achievable = the library's streaming-read kernel over
+    the same weight replicas, timed the same way (the rate a pure read of a
+    buffer that size reaches on this part).
 The CPU baseline is the oracle's restatement of the reference NumPy path
 (examples/38_quantized_matmul.py:215-232), timed on this host on the same
 inputs, median of timed runs after warm-up as in
@@ -185,16 +189,21 @@ class Stack:
                 raise RuntimeError(f"launch failed: {rc}")
 
 
-def time_graph(case, steps, warmup, per_graph=None):
-    """Capture `per_graph` launches in a graph; replay to cover warmup + steps.
+def time_graph(case, steps, warmup, trials=21, per_graph=None):
+    """Median time of one launch, from `trials` replays of a graph of launches.
 
-    Returns (seconds for `steps` launches, launches actually timed)."""
+    `warmup` eager launches come first (first-launch costs), then `per_graph`
+    launches (default `steps`, rotating the case's weight replicas) are
+    captured in one HIP graph, replayed once untimed, then replayed `trials`
+    times with a HIP event recorded on the capture stream before each replay
+    and after the last, all enqueued back to back.  Returns (median seconds
+    per launch, {"trials", "launches_per_trial", "min_us", "max_us"})."""
     import torch
-    per_graph = per_graph or case.R * max(1, math.ceil(64 / case.R))
+    per_graph = max(1, per_graph or steps)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for i in range(min(per_graph, 2 * case.R)):   # eager warm-up (first-launch costs)
+        for i in range(max(1, warmup)):
             case.launch(i, ctypes.c_void_p(s.cuda_stream))
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -202,20 +211,40 @@ def time_graph(case, steps, warmup, per_graph=None):
         for i in range(per_graph):
             case.launch(i, ctypes.c_void_p(s.cuda_stream))
     torch.cuda.synchronize()
-    n_warm = max(1, math.ceil(warmup / per_graph))
-    n_timed = max(1, math.ceil(steps / per_graph))
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(trials + 1)]
     with torch.cuda.stream(s):
-        for _ in range(n_warm):
-            g.replay()
+        g.replay()
         torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for _ in range(n_timed):
+        ev[0].record(s)
+        for t in range(trials):
             g.replay()
-        e1.record(s)
+            ev[t + 1].record(s)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3, n_timed * per_graph
+    per = sorted(ev[t].elapsed_time(ev[t + 1]) / 1e3 / per_graph for t in range(trials))
+    med = per[len(per) // 2]
+    del g
+    return med, {"trials": trials, "launches_per_trial": per_graph,
+                 "min_us": round(per[0] * 1e6, 3), "max_us": round(per[-1] * 1e6, 3)}
+
+
+class StreamCase:
+    """The library's streaming-read kernel over a case's weight replicas: the
+    achievable HBM read rate for a buffer of that size on this part."""
+
+    def __init__(self, case):
+        import torch
+        from locomp_amd import _lib
+        self.W, self.R = case.W, case.R
+        self.nbytes = case.W[0].numel() // 1024 * 1024
+        self.sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+        self.lib = _lib.load()
+
+    def launch(self, i, stream):
+        rc = self.lib.locomp_amd_stream_read(ctypes.c_void_p(self.W[i % self.R].data_ptr()),
+                                             self.nbytes, ctypes.c_void_p(self.sink.data_ptr()),
+                                             stream)
+        if rc != 0:
+            raise RuntimeError(f"stream_read failed: {rc}")
 
 
 def cpu_baseline(case, budget_s=20.0):
@@ -234,8 +263,8 @@ def cpu_baseline(case, budget_s=20.0):
     t0 = time.perf_counter()
     run()
     one = time.perf_counter() - t0
-    runs = int(max(3, min(15, budget_s / max(one, 1e-3) - 2)))
-    for _ in range(2):
+    runs = int(max(3, min(15, budget_s / max(one, 1e-3) - 5)))
+    for _ in range(5):
         run()
     ts = []
     for _ in range(runs):
@@ -248,7 +277,7 @@ def cpu_baseline(case, budget_s=20.0):
         "cores": int(blas_threads),
         "kind": "port",
         "sample": (f"oracle fast_numpy_matvec_int4 (examples/38_quantized_matmul.py:215-232) on the "
-                   f"full M=1 x 4096 x 11008 g128 inputs, median of {runs} runs after 2 warm-ups, "
+                   f"full M=1 x 4096 x 11008 g128 inputs, median of {runs} runs after 5 warm-ups, "
                    f"{med * 1e3:.1f} ms/call; elementwise NumPy is single-threaded, the BLAS "
                    f"product used {blas_threads} threads; host os.cpu_count()={os.cpu_count()}, "
                    f"affinity={len(os.sched_getaffinity(0))}"),
@@ -308,8 +337,8 @@ def sweep():
                 cells = []
                 for M in SWEEP_M:
                     case = Case("matvec", wb, M, N, K, G, 0.001, 0.01, max_replicas=16)
-                    t, n = time_graph(case, 200, 20)
-                    cells.append(f"{t / n * 1e6:.1f}")
+                    t, _ = time_graph(case, max(20, case.R), 5, trials=11)
+                    cells.append(f"{t * 1e6:.1f}")
                     del case
                     torch.cuda.empty_cache()
                 print(f"| {wb} | {N} | {K} | {G} | " + " | ".join(cells) + " |", flush=True)
@@ -319,8 +348,9 @@ def sweep():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000)
-    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--steps", type=int, default=200,
+                    help="launches per timed trial (the headline's median is over 21 trials)")
+    ap.add_argument("--warmup", type=int, default=20, help="eager launches before capture")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra cases to run (default all)")
     ap.add_argument("--profile", default="", choices=["", "gemv", "gemv_m16", "gemm", "dequant", "w8a16", "copy"],
@@ -347,9 +377,13 @@ def main():
     c3 = synth.CFG3
     log("case gemv_w4a16 M=1")
     head = Case("matvec", 4, 1, c3["N"], c3["K"], c3["G"], c3["lo"], c3["hi"])
-    t, n = time_graph(head, args.steps, args.warmup)
-    us = t / n * 1e6
-    gbs = head.algo_bytes / (t / n) / 1e9
+    t, tinfo = time_graph(head, args.steps, args.warmup)
+    us = t * 1e6
+    gbs = head.algo_bytes / t / 1e9
+    log("case stream_read (achievable HBM read rate, same weight replicas)")
+    sc = StreamCase(head)
+    ts, sinfo = time_graph(sc, args.steps, args.warmup)
+    stream_gbs = sc.nbytes / ts / 1e9
 
     extra = {}
     only = set(filter(None, args.only.split(","))) if args.only else None
@@ -358,11 +392,9 @@ def main():
         return only is None or name in only
 
     def run_case(name, case, bound):
-        steps = max(200, args.steps // 8)
-        tt, nn = time_graph(case, steps, max(50, args.warmup // 8))
-        per = tt / nn
+        per, info = time_graph(case, max(20, case.R), 5)
         d = {"us_per_launch": round(per * 1e6, 3), "GB_s": round(case.algo_bytes / per / 1e9, 1),
-             "replicas": case.R, "launches": nn}
+             "replicas": case.R, **info}
         if case.flops:
             d["TFLOP_s"] = round(case.flops / per / 1e12, 2)
         if bound == "hbm":
@@ -400,8 +432,7 @@ def main():
     if want("smollm2"):
         for fused, silu in ((False, False), (True, False), (True, True)):
             st = Stack(fused=fused, silu=silu)
-            tt, nn = time_graph(st, 40, 5, per_graph=4)
-            per = tt / nn
+            per, _ = time_graph(st, 4, 1)
             d = {"us_per_token": round(per * 1e6, 2), "GB_s": round(st.algo_bytes / per / 1e9, 1),
                  "gemvs_per_token": len(st.layers), "algorithmic_bytes": st.algo_bytes,
                  "us_per_gemv": round(per * 1e6 / len(st.layers), 3)}
@@ -426,8 +457,9 @@ def main():
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": n,
+        "steps": args.steps,
         "warmup": args.warmup,
+        "trials": tinfo["trials"],
         "ms_per_step": round(us / 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -440,7 +472,13 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": head.algo_bytes,
-                     "avg_launch_us": round(us, 3)},
+                     "median_launch_us": round(us, 3), "min_launch_us": tinfo["min_us"],
+                     "max_launch_us": tinfo["max_us"],
+                     "achievable": round(stream_gbs, 1),
+                     "achievable_note": (f"stream_read of the same {sc.nbytes} B weight replicas, "
+                                         f"{ts * 1e6:.3f} us per launch, median of "
+                                         f"{sinfo['trials']} trials"),
+                     "frac_of_achievable": round(gbs / stream_gbs, 4)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -170,6 +170,13 @@ int locomp_amd_quantize_int4(const void* W, void* PACKED, float* SCALES, int64_t
 int locomp_amd_quantize_int8(const void* W, void* Q, float* SCALES, int64_t N, int64_t K,
                              int64_t GROUP_SIZE, int in_dtype, void* stream);
 
+/* Measurement helper, no counterpart in the reference: stream-read `bytes`
+ * (a multiple of 1024, below 2^31) of device memory at `buf` and discard it
+ * (`sink`: 4 bytes of device memory, written only on a value random data does
+ * not produce).  The achievable HBM read rate for a buffer of that size, the
+ * ceiling the bandwidth-bound kernels above are compared against. */
+int locomp_amd_stream_read(const void* buf, int64_t bytes, void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,7 @@ SIGNATURES = {
                                                 _i64, _int, _int, _int, _vp],
     "locomp_amd_quantize_int4": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp],
     "locomp_amd_quantize_int8": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
+    "locomp_amd_stream_read": [_vp, _i64, _vp, _vp],
 }
 
 _lib = None
