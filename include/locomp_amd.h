@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define LOCOMP_AMD_ABI_VERSION 3
+#define LOCOMP_AMD_ABI_VERSION 4
 
 /* Element dtype codes. */
 enum {
@@ -59,7 +59,8 @@ enum {
   LQ_ERR_SHAPE = -1,   /* inconsistent or unsupported sizes           */
   LQ_ERR_DTYPE = -2,   /* unknown dtype code                          */
   LQ_ERR_NULL = -3,    /* null pointer with a non-empty problem        */
-  LQ_ERR_POLICY = -4   /* unknown kernel policy                        */
+  LQ_ERR_POLICY = -4,  /* unknown kernel policy                        */
+  LQ_ERR_SCRATCH = -5  /* needs more scratch than the fixed buffer holds */
 };
 
 /* Quantizer variants (locomp_amd_quantize_int4). */
@@ -120,6 +121,24 @@ int locomp_amd_dequant_matvec_int4(const void* X, const void* W,
                                    int64_t N, int64_t M, int x_dtype,
                                    int scale_dtype, int out_dtype,
                                    void* stream);
+
+/* As locomp_amd_dequant_matvec_int4, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same kernels and
+ * results; the split-K prefill's fp32 partials go to a fixed 32 MiB array in
+ * the library's device memory (one per GPU, held until the process ends)
+ * instead of the per-stream workspace, and the call allocates nothing.  A
+ * call whose split-K plan needs more (M x N x 4 bytes x splits: e.g. beyond
+ * M = 512 at N = 4096) returns LQ_ERR_SCRATCH and launches nothing.  All calls
+ * on one GPU share its array: calls that overlap in time on one GPU (several
+ * streams or threads) race and must be serialised by the caller. */
+int locomp_amd_dequant_matvec_int4_noalloc(const void* X, const void* W,
+                                           const void* scales, void* O,
+                                           int64_t K_dim, int64_t HALF_K,
+                                           int64_t NUM_SCALES, int64_t GROUP_SIZE,
+                                           int64_t N, int64_t M, int x_dtype,
+                                           int scale_dtype, int out_dtype,
+                                           void* stream);
 
 /* O [M, N] = X [M, K] @ dequant_int8(W)^T, fp32 accumulation.
  * Replaces locomp_launch_dequant_matvec_int8 generated for

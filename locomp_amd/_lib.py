@@ -13,12 +13,12 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_liblocomp_amd.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # dtype codes (LQ_F32 / LQ_F16 / LQ_BF16)
 F32, F16, BF16 = 0, 1, 2
 # error codes
-OK, ERR_SHAPE, ERR_DTYPE, ERR_NULL, ERR_POLICY = 0, -1, -2, -3, -4
+OK, ERR_SHAPE, ERR_DTYPE, ERR_NULL, ERR_POLICY, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
 # kernel policies
 POLICY_AUTO, POLICY_GENERIC = 0, 1
 # quantizer variants (LQ_QUANT_EX38 / LQ_QUANT_EX52)
@@ -38,6 +38,8 @@ SIGNATURES = {
     "locomp_amd_dequant_int8": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp],
     "locomp_amd_dequant_matvec_int4": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                        _int, _int, _int, _vp],
+    "locomp_amd_dequant_matvec_int4_noalloc": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                               _i64, _int, _int, _int, _vp],
     "locomp_amd_dequant_matvec_int8": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                        _int, _int, _int, _vp],
     "locomp_amd_dequant_matvec_int4_silu_mul": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

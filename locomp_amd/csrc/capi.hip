@@ -17,7 +17,7 @@ int launch_generic(const void*, const void*, const void*, void*, int64_t, int64_
                    int, int, int, hipStream_t);
 template <int WBITS>
 int launch_gemm(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
-                int, int, hipStream_t);
+                int, int, hipStream_t, const FixedScratch*);
 int launch_zero_fill(void*, int64_t, int, hipStream_t);
 int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
                     hipStream_t);
@@ -53,9 +53,12 @@ static bool fast_allowed() { return g_policy.load(std::memory_order_relaxed) == 
 using namespace lq;
 
 // Kernel choice for the dequant-matmul entries (WBITS = 4 or 8).
+// `fixed`: scratch lent by the caller for split-K partials (no allocation);
+// nullptr = the per-stream workspace.
 template <int WBITS>
 static int matmul_dispatch(const void* X, const void* W, const void* S, void* O, int64_t K,
-                           int64_t G, int64_t N, int64_t M, int xd, int sd, int od, hipStream_t st) {
+                           int64_t G, int64_t N, int64_t M, int xd, int sd, int od, hipStream_t st,
+                           const FixedScratch* fixed = nullptr) {
   if (!dtype_ok(xd) || !dtype_ok(sd) || !dtype_ok(od)) return LQ_ERR_DTYPE;
   if (M < 0) return LQ_ERR_SHAPE;
   if (M == 0 || N == 0) return LQ_OK;
@@ -80,7 +83,7 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
     // stream without the workspace that needs, takes the generic kernel).
     const bool gemm_ok = WBITS == 4 ? G % 32 == 0 : G % 64 == 0;
     if (M > 64 && K % 64 == 0 && gemm_ok) {
-      const int rc = launch_gemm<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
+      const int rc = launch_gemm<WBITS>(X, W, S, O, M, N, K, G, sd, od, st, fixed);
       if (rc != LQ_ERR_SHAPE) return rc;
     }
   }
@@ -98,6 +101,7 @@ const char* locomp_amd_strerror(int code) {
     case LQ_ERR_DTYPE: return "unknown dtype code";
     case LQ_ERR_NULL: return "null pointer for a non-empty problem";
     case LQ_ERR_POLICY: return "unknown kernel policy";
+    case LQ_ERR_SCRATCH: return "problem needs more scratch than the fixed buffer holds";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -152,6 +156,26 @@ int locomp_amd_dequant_matvec_int4(const void* X, const void* W, const void* sca
   if (HALF_K * 2 != K_dim) return LQ_ERR_SHAPE;
   return matmul_dispatch<4>(X, W, scales, O, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
                             out_dtype, static_cast<hipStream_t>(stream));
+}
+
+int locomp_amd_dequant_matvec_int4_noalloc(const void* X, const void* W, const void* scales,
+                                           void* O, int64_t K_dim, int64_t HALF_K,
+                                           int64_t NUM_SCALES, int64_t GROUP_SIZE, int64_t N,
+                                           int64_t M, int x_dtype, int scale_dtype, int out_dtype,
+                                           void* stream) {
+  int rc = check_common(K_dim, NUM_SCALES, GROUP_SIZE, N);
+  if (rc) return rc;
+  if (HALF_K * 2 != K_dim) return LQ_ERR_SHAPE;
+  FixedScratch fixed{nullptr, kStaticScratchBytes};
+  // the device's scratch address (looked up on the device's first call that
+  // may launch; argument errors and empty problems return before)
+  if (dtype_ok(x_dtype) && dtype_ok(scale_dtype) && dtype_ok(out_dtype) && M > 0 && N > 0 &&
+      K_dim > 0 && X && W && scales && O) {
+    rc = static_scratch(&fixed.p);
+    if (rc != LQ_OK) return rc;
+  }
+  return matmul_dispatch<4>(X, W, scales, O, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
+                            out_dtype, static_cast<hipStream_t>(stream), &fixed);
 }
 
 int locomp_amd_dequant_matvec_int8(const void* X, const void* W, const void* scales, void* O,

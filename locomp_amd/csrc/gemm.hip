@@ -461,6 +461,38 @@ void* stream_workspace(int slot, size_t bytes, hipStream_t st) {
 }
 static void* split_workspace(size_t bytes, hipStream_t st) { return stream_workspace(0, bytes, st); }
 
+// Fixed split-K scratch for callers that cannot allocate (the _noalloc entry
+// point): one array per device, held by the loaded code object until the
+// process ends.  Host code must use the per-device address from
+// hipGetSymbolAddress, never `scratch` itself (in host code that name is a
+// host-side stand-in, not a device address).  Every call on a device shares
+// the device's array: calls that overlap on one device race.  The split-K
+// kernels write every element of the slices they read back, so nothing has to
+// be cleared between calls.
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+int static_scratch(void** ptr) {
+  constexpr int kMaxDev = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDev] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return int(e);
+  if (dev < 0 || dev >= kMaxDev) return LQ_ERR_SCRATCH;
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return e != hipSuccess ? int(e) : LQ_ERR_SCRATCH;
+    }
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return LQ_OK;
+}
+
 template <int OD>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ P,
                                                            void* __restrict__ O, size_t mn,
@@ -534,11 +566,18 @@ static int choose_splits(int64_t tiles, int64_t K, int need) {
 
 template <class C, int WBITS, int SD, int OD, bool EPI = false>
 static int launch_gemm_split(const void* X, const void* W, const void* S, void* O, int64_t M,
-                             int64_t N, int64_t K, int64_t G, int splits, hipStream_t st) {
+                             int64_t N, int64_t K, int64_t G, int splits, hipStream_t st,
+                             const FixedScratch* fixed) {
   const size_t mn = size_t(M) * size_t(N);
   const size_t ws_bytes = mn * sizeof(float) * size_t(splits);
-  void* ws = ws_bytes <= kSplitWsMax ? split_workspace(ws_bytes, st) : nullptr;
-  if (ws == nullptr) return LQ_ERR_SHAPE;
+  void* ws;
+  if (fixed != nullptr) {   // caller-provided scratch: never allocate
+    if (ws_bytes > fixed->bytes) return LQ_ERR_SCRATCH;
+    ws = fixed->p;
+  } else {
+    ws = ws_bytes <= kSplitWsMax ? split_workspace(ws_bytes, st) : nullptr;
+    if (ws == nullptr) return LQ_ERR_SHAPE;
+  }
   int rc = launch_gemm_cfg<C, WBITS, SD, LQ_F32>(X, W, S, ws, M, N, K, G, splits, st);
   if (rc != LQ_OK) return rc;
   if constexpr (EPI)
@@ -553,7 +592,8 @@ static int launch_gemm_split(const void* X, const void* W, const void* S, void* 
 // LQ_ERR_SHAPE: no configuration applies (the caller takes another kernel).
 template <int WBITS, int SD, int OD, bool EPI = false>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
-                         int64_t N, int64_t K, int64_t G, hipStream_t st) {
+                         int64_t N, int64_t K, int64_t G, hipStream_t st,
+                         const FixedScratch* fixed = nullptr) {
   const int need = min_splits<WBITS>(K, G);
   if (need == 0) return LQ_ERR_SHAPE;
   // 256-row tiles only when they alone give every CU (256) a tile; below that
@@ -563,19 +603,19 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
                             ((N + GemmDefault::BN - 1) / GemmDefault::BN);
   if (big_tiles >= 256) {
     if (need == 1) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 1, st);
-    return launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, need, st);
+    return launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, need, st, fixed);
   }
   // Half the CUs or more with 256-row tiles: those tiles with k split in two
   // beat twice as many 128-row tiles (M = 1024 at N = 4096: 62.7 -> 56.9 us).
   if (big_tiles >= 128 && need <= 2 && (K / kBK) % 2 == 0 && K / kBK >= 8) {
-    const int rc = launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 2, st);
+    const int rc = launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 2, st, fixed);
     if (rc != LQ_ERR_SHAPE || need > 1) return rc;
   }
   const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
                         ((N + GemmSmall::BN - 1) / GemmSmall::BN);
   const int splits = choose_splits(tiles, K, need);
   if (splits > 1) {
-    const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, splits, st);
+    const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, splits, st, fixed);
     if (rc != LQ_ERR_SHAPE || need > 1) return rc;
   }
   return launch_gemm_cfg<GemmSmall, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 1, st);
@@ -583,9 +623,9 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
 
 template <int WBITS>
 int launch_gemm(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
-                int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+                int64_t K, int64_t G, int sd, int od, hipStream_t st, const FixedScratch* fixed) {
 #define LQ_GM(SD_, OD_) \
-  if (sd == SD_ && od == OD_) return launch_gemm_t<WBITS, SD_, OD_>(X, W, S, O, M, N, K, G, st)
+  if (sd == SD_ && od == OD_) return launch_gemm_t<WBITS, SD_, OD_>(X, W, S, O, M, N, K, G, st, fixed)
   LQ_GM(LQ_F16, LQ_F16);
   LQ_GM(LQ_F16, LQ_F32);
   LQ_GM(LQ_F16, LQ_BF16);
@@ -626,8 +666,8 @@ int launch_gemm_silu(const void* X, const void* W, const void* S, void* O, int64
 }
 
 template int launch_gemm<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
-                            int64_t, int64_t, int, int, hipStream_t);
+                            int64_t, int64_t, int, int, hipStream_t, const FixedScratch*);
 template int launch_gemm<8>(const void*, const void*, const void*, void*, int64_t, int64_t,
-                            int64_t, int64_t, int, int, hipStream_t);
+                            int64_t, int64_t, int, int, hipStream_t, const FixedScratch*);
 
 }  // namespace lq

@@ -166,6 +166,19 @@ __device__ __forceinline__ u32x4_t xperm8(u32x4_t d) {
 
 // ---------------------------------------------------------------- launch --
 
+// Device memory a caller lends the split-K prefill instead of the per-stream
+// workspace (which allocates): p holds `bytes` bytes.
+struct FixedScratch {
+  void* p;
+  size_t bytes;
+};
+// Size of the fixed split-K scratch array behind the _noalloc entry point:
+// enough for the splits chosen at M <= 512 x N <= 4096 (and M <= 128 x
+// N <= 16384); larger splits are rejected with LQ_ERR_SCRATCH.
+constexpr size_t kStaticScratchBytes = size_t(32) << 20;
+// Per-device address of that array (looked up once per device).
+int static_scratch(void** ptr);
+
 __host__ __forceinline__ int check_launch() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LQ_OK : int(e);

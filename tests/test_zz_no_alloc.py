@@ -1,0 +1,64 @@
+"""GPU: the allocation-free dequant-matvec entry point
+(locomp_amd_dequant_matvec_int4_noalloc) against the allocating one
+(locomp_amd_dequant_matvec_int4), through the C ABI on the same inputs.
+
+Both run the same kernels; the split-K prefill partials of the first live in
+the library's fixed per-GPU scratch array, so the outputs must be bit-identical,
+including on a second, smaller call right after the first (the array keeps the
+first call's contents)."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from locomp_amd import _lib, synth
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+vp = ctypes.c_void_p
+
+
+def _run(fn, X, W, S, M, N, K, G):
+    stream = torch.cuda.current_stream()
+    Xd, Wd, Sd = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (X, W, S))
+    Od = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+    rc = fn(vp(Xd.data_ptr()), vp(Wd.data_ptr()), vp(Sd.data_ptr()), vp(Od.data_ptr()),
+            K, K // 2, K // G, G, N, M, _lib.F16, _lib.F16, _lib.F16, vp(stream.cuda_stream))
+    torch.cuda.synchronize()
+    return rc, Od.cpu().numpy()
+
+
+# (M, N, K, G) pairs: a split-K prefill, then a smaller one; decode shapes need
+# no scratch and must match too
+CASES = [
+    ((128, 4096, 4096, 128), (100, 2048, 4096, 128)),   # 8-way split, then 4-way
+    ((512, 4096, 4096, 128), (200, 1024, 2048, 64)),
+    ((1, 11008, 4096, 128), (4, 4096, 4096, 32)),
+]
+
+
+@pytest.mark.parametrize("first,second", CASES)
+def test_noalloc_matches_allocating_entry(first, second):
+    lib = _lib.load()
+    for seed, (M, N, K, G) in enumerate((first, second)):
+        print(f"noalloc case M={M} N={N} K={K} G={G}", flush=True)
+        X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=seed)
+        rc_a, want = _run(lib.locomp_amd_dequant_matvec_int4, X, W, S, M, N, K, G)
+        rc_b, got = _run(lib.locomp_amd_dequant_matvec_int4_noalloc, X, W, S, M, N, K, G)
+        assert rc_a == 0 and rc_b == 0, (rc_a, rc_b)
+        assert not np.isnan(got).any()
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_noalloc_rejects_plans_beyond_the_scratch():
+    # 768 x 8192 takes 256-row tiles with k split in two: 768 * 8192 * 4 * 2 B
+    # = 48 MiB of partials, more than the fixed 32 MiB array
+    lib = _lib.load()
+    M, N, K, G = 768, 8192, 4096, 128
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=3)
+    rc, _ = _run(lib.locomp_amd_dequant_matvec_int4_noalloc, X, W, S, M, N, K, G)
+    assert rc == _lib.ERR_SCRATCH
+    rc, _ = _run(lib.locomp_amd_dequant_matvec_int4, X, W, S, M, N, K, G)
+    assert rc == 0
