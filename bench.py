@@ -57,34 +57,44 @@ class Case:
     """One dequant-matmul / dequant configuration with device replicas."""
 
     def __init__(self, kind, wbits, M, N, K, G, lo, hi, seed=0, min_bytes=LLC_BYTES * 5 // 4,
-                 max_replicas=64):
+                 max_replicas=64, xd="f16"):
+        """xd: activation dtype "f16" (fp16 scales and outputs), "bf16" (fp16
+        scales, bf16 outputs) or "f32" (fp32 scales and outputs, the
+        reference's own dtypes)."""
         import torch
         from locomp_amd import synth, _lib
         self.kind, self.wbits, self.M, self.N, self.K, self.G = kind, wbits, M, N, K, G
+        self.codes = {"f16": (1, 1, 1), "bf16": (2, 1, 2), "f32": (0, 0, 0)}[xd]
+        xt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[xd]
         if kind == "dequant":
             W, S = synth.dequant_case(wbits, N, K, G, lo, hi, seed=seed)
             X = None
         else:
             X, W, S = synth.matvec_case(wbits, M, N, K, G, lo, hi, seed=seed)
+            if xd == "f32":
+                S = S.astype(np.float32)
         self.host = (X, W, S)
         self.w_bytes = W.nbytes
         self.s_bytes = S.nbytes
+        esz = 4 if xd == "f32" else 2
         if kind == "dequant":
             self.out_elems = N * K
             self.algo_bytes = W.nbytes + S.nbytes + N * K * 2
             self.flops = 0
         else:
             self.out_elems = M * N
-            self.algo_bytes = W.nbytes + S.nbytes + X.nbytes + M * N * 2
+            self.algo_bytes = W.nbytes + S.nbytes + M * K * esz + M * N * esz
             self.flops = 2 * M * N * K
         per = W.nbytes + S.nbytes + (self.out_elems * 2 if kind == "dequant" else 0)
         self.R = max(1, min(max_replicas, math.ceil(min_bytes / per)))
         w0, s0 = _dev(W), _dev(S)
         self.W = [w0] + [w0.clone() for _ in range(self.R - 1)]
         self.S = [s0] + [s0.clone() for _ in range(self.R - 1)]
-        self.X = _dev(X) if X is not None else None
+        self.X = _dev(X.astype(np.float32)).to(xt) if X is not None else None
         nout = self.R if kind == "dequant" else 1
-        self.O = [torch.empty(self.out_elems, dtype=torch.float16, device="cuda") for _ in range(nout)]
+        ot = torch.float16 if kind == "dequant" else {"f16": torch.float16, "bf16": torch.bfloat16,
+                                                       "f32": torch.float32}[xd]
+        self.O = [torch.empty(self.out_elems, dtype=ot, device="cuda") for _ in range(nout)]
         self.lib = _lib.load()
         torch.cuda.synchronize()
 
@@ -99,11 +109,11 @@ class Case:
         elif self.wbits == 4:
             rc = lib.locomp_amd_dequant_matvec_int4(
                 vp(self.X.data_ptr()), vp(self.W[r].data_ptr()), vp(self.S[r].data_ptr()),
-                vp(self.O[0].data_ptr()), K, K // 2, K // G, G, N, M, 1, 1, 1, stream)
+                vp(self.O[0].data_ptr()), K, K // 2, K // G, G, N, M, *self.codes, stream)
         else:
             rc = lib.locomp_amd_dequant_matvec_int8(
                 vp(self.X.data_ptr()), vp(self.W[r].data_ptr()), vp(self.S[r].data_ptr()),
-                vp(self.O[0].data_ptr()), K, K // G, G, N, M, 1, 1, 1, stream)
+                vp(self.O[0].data_ptr()), K, K // G, G, N, M, *self.codes, stream)
         if rc != 0:
             raise RuntimeError(f"launch failed: {rc}")
 
@@ -423,6 +433,16 @@ def main():
         if want(f"gemv_m{M}"):
             run_case(f"gemv_w4a16_M{M}", Case("matvec", 4, M, c3["N"], c3["K"], c3["G"], c3["lo"],
                                                 c3["hi"]), "hbm")
+    for xd in ("bf16", "f32"):
+        for M in ((1, 4, 16) if xd == "bf16" else (1, 4)):
+            if want(f"gemv_{xd}"):
+                run_case(f"gemv_w4a{xd}_M{M}", Case("matvec", 4, M, c3["N"], c3["K"], c3["G"],
+                                                              c3["lo"], c3["hi"], xd=xd), "hbm")
+    if want("gemm_prefill_bf16"):
+        c = synth.CFG5A
+        run_case("gemm_prefill_w4abf16_2048x4096x4096_g128",
+                 Case("matvec", 4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
+                      min_bytes=0, max_replicas=4, xd="bf16"), "mfma")
     if want("dequant"):
         c = synth.CFG2
         run_case("dequant_int4_4096x4096_g32_f16",

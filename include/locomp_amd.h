@@ -111,6 +111,11 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * NUM_SCALES, GROUP_SIZE; grid (N,), launched at
  * examples/38_quantized_matmul.py:154).  M = 1 is the reference's matvec;
  * M <= 64 runs the decode (skinny) kernel, larger M the prefill MFMA GEMM.
+ * Activations may be fp16, bf16 or fp32 (the reference's dtype): fp16 and
+ * bf16 run on fp16 / bf16 matrix cores at every M; fp32 at M <= 4 runs on
+ * bf16 matrix cores as three exact bf16 parts; other fp32 shapes take a
+ * generic kernel.  The fast kernels need X and W 16-byte aligned and the
+ * scales 4-byte aligned (otherwise a generic kernel runs).
  * A prefill GEMM with fewer output tiles than CUs splits K and keeps an fp32
  * workspace per (device, stream), allocated on first use and held until the
  * process ends (int4 and int8 alike). */

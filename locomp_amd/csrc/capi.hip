@@ -13,6 +13,12 @@ template <int WBITS>
 int launch_skinny(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
                   int, int, hipStream_t);
 template <int WBITS>
+int launch_gemm_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
+                  int, int, int, hipStream_t, const FixedScratch*);
+template <int WBITS>
+int launch_skinny_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                    int64_t, int, int, int, hipStream_t);
+template <int WBITS>
 int launch_generic(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
                    int, int, int, hipStream_t);
 template <int WBITS>
@@ -68,8 +74,20 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
   const int64_t row_bytes = WBITS == 4 ? K / 2 : K;
   const bool small_enough = M * K <= kMax32 && N * row_bytes <= kMax32 && M * N <= kMax32 &&
                             N * (K / G) <= kMax32;
-  const bool fast = fast_allowed() && xd == LQ_F16 && small_enough && aligned(X, 16) &&
-                    aligned(W, 16) && K % 8 == 0;
+  // the fast kernels stage scale rows as dwords and load 16-byte pieces
+  const bool fast_common = fast_allowed() && small_enough && aligned(X, 16) && aligned(W, 16) &&
+                           aligned(S, 4) && K % 8 == 0;
+  if (fast_common && (xd == LQ_BF16 || xd == LQ_F32) && M <= 16) {
+    // bf16 activations (M <= 16) and fp32 (M <= 4) on bf16 MFMAs
+    const int rc = launch_skinny_x<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
+  if (fast_common && xd == LQ_BF16 && M > 16 && K % 64 == 0) {
+    // bf16 prefill: the MFMA GEMM on exact integer weights (G % 64)
+    const int rc = launch_gemm_x<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st, fixed);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
+  const bool fast = fast_common && xd == LQ_F16;
   if (fast) {
     // Skinny (decode) kernel: 16-byte weight chunks per lane must lie in one
     // group and in one row.
@@ -205,6 +223,7 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
   if (!X || !W || !scales) return LQ_ERR_NULL;
   const int64_t N = 2 * I;
   const bool fast = fast_allowed() && x_dtype == LQ_F16 && aligned(X, 16) && aligned(W, 16) &&
+                    aligned(scales, 4) &&
                     M * K_dim <= kMax32 && N * HALF_K <= kMax32 && N * NUM_SCALES <= kMax32 &&
                     scale_dtype != LQ_BF16 && out_dtype != LQ_BF16;
   if (fast) {

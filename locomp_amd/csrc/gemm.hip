@@ -40,6 +40,7 @@
 namespace lq {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kBK = 64;
 
@@ -87,20 +88,25 @@ constexpr int kBStages = 2;
 
 // EPI: gate/up rows interleaved (2i, 2i + 1); store silu(gate) * up to
 // O [M, N / 2] (columns n and n + 1 sit in lanes r16 and r16 ^ 1).
-template <class C, int WBITS, int SD, int OD, bool EPI = false>
+// XD: activation dtype, fp16 (fp16 MFMA) or bf16 (bf16 MFMA; B holds the
+// exact integers q - 8 / q as bf16 and the scales are applied in fp32, like
+// int8).  SD / OD = kRT take the scale / output dtype from sd_rt / od_rt.
+template <class C, int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int tiles_m, int tiles_n,
-    int kspan) {
+    int kspan, int sd_rt = 0, int od_rt = 0) {
   constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN;
   static_assert(BM % (8 * C::kWaves) == 0, "A DMA: whole 1 KB instructions per wave");
-  typedef typename Elem<SD>::T stype;
+  constexpr bool kBf = XD == LQ_BF16;
+  typedef typename Elem<SD == kRT ? LQ_F32 : SD>::T stype;
   __shared__ __attribute__((aligned(16))) half_t As[kAStages][BM * kBK];
   __shared__ __attribute__((aligned(16))) half_t Bs[kBStages][BN * kBK];
-  // int8: B holds the exact integers q and the group scales are applied to
-  // fp32 partial sums (a pre-scaled fp16 weight would round |q s| up to 2.5
-  // to 11 bits, too coarse at K = 4096); the tile's scale rows live here.
-  constexpr bool kPost = WBITS == 8;
+  // int8 (and bf16 activations): B holds the exact integers and the group
+  // scales are applied to fp32 partial sums (a pre-scaled fp16 weight would
+  // round |q s| up to 2.5 to 11 bits, too coarse at K = 4096; bf16 keeps 8);
+  // the tile's scale rows live here.
+  constexpr bool kPost = WBITS == 8 || kBf;
   __shared__ float Ssh[kPost ? kGemmScaleFloats : 1];
 
   const int tid = threadIdx.x;
@@ -199,7 +205,48 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const half_t hs = half_t(bs);
     const half2_t s2 = {hs, hs};
     half_t* dst = Bs[stage];
-    if constexpr (WBITS == 4) {
+    if constexpr (kBf) {
+      // exact integers as bf16: an integer of at most 8 significant bits is
+      // exact as a float, whose high half is then its bf16 pattern
+      (void)s2;
+      auto pack = [](float lo, float hi) {
+        return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+      };
+      if constexpr (WBITS == 4) {
+#pragma unroll
+        for (int i = 0; i < kBWords; ++i) {
+          const uint32_t e = bq[i] & 0x0F0F0F0Fu, o = (bq[i] >> 4) & 0x0F0F0F0Fu;
+          float f[8];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            f[2 * b] = float((e >> (8 * b)) & 0xFFu) - 8.0f;       // k = 2 b
+            f[2 * b + 1] = float((o >> (8 * b)) & 0xFFu) - 8.0f;   // k = 2 b + 1
+          }
+          u32x4_t v;
+          v.x = pack(f[0], f[1]);
+          v.y = pack(f[2], f[3]);
+          v.z = pack(f[4], f[5]);
+          v.w = pack(f[6], f[7]);
+          *reinterpret_cast<u32x4_t*>(dst + b_lds_off(b_n, b_part * kBWords + i)) = v;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kBWords / 2; ++i) {
+          float f[8];
+#pragma unroll
+          for (int b = 0; b < 8; ++b) {
+            const uint32_t u = bq[2 * i + (b >> 2)] ^ 0x80808080u;
+            f[b] = float((u >> (8 * (b & 3))) & 0xFFu) - 128.0f;
+          }
+          u32x4_t v;
+          v.x = pack(f[0], f[1]);
+          v.y = pack(f[2], f[3]);
+          v.z = pack(f[4], f[5]);
+          v.w = pack(f[6], f[7]);
+          *reinterpret_cast<u32x4_t*>(dst + b_lds_off(b_n, b_part * (kBWords / 2) + i)) = v;
+        }
+      }
+    } else if constexpr (WBITS == 4) {
       // one dword = 8 k = one 16-byte LDS chunk
 #pragma unroll
       for (int i = 0; i < kBWords; ++i) {
@@ -248,7 +295,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     for (int idx = tid; idx < BN * ns; idx += C::kThreads) {
       const int row = idx / ns;
       const int n = min(n0 + row, N - 1);
-      Ssh[idx] = load_f32<SD>(S, size_t(n) * num_scales + g0 + (idx - row * ns));
+      Ssh[idx] = load_f32_rt<SD>(S, size_t(n) * num_scales + g0 + (idx - row * ns), sd_rt);
     }
   }
 
@@ -287,7 +334,10 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        if constexpr (kPost)
+        if constexpr (kBf)
+          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf8_t, fa[i]), __builtin_bit_cast(bf8_t, fb[j]), part[i][j], 0, 0, 0);
+        else if constexpr (kPost)
           part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], part[i][j], 0, 0, 0);
         else
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
@@ -385,9 +435,9 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
           const float g = acc[i][j][r];
           const float up = __shfl_xor(g, 1, 64);
           if ((r16 & 1) == 0 && m < M && n < N)
-            store_f32<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up);
+            store_out<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up, od_rt);
         } else {
-          if (m < M && n < N) store_f32<OD>(O, obase + size_t(m) * N + n, acc[i][j][r]);
+          if (m < M && n < N) store_out<OD>(O, obase + size_t(m) * N + n, acc[i][j][r], od_rt);
         }
       }
     }
@@ -399,15 +449,16 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #endif
 typedef GemmCfg<LQ_GEMM_CFG> GemmDefault;   // default: 256 x 128 tile, 8 waves of 32 x 128
 
-template <class C, int WBITS, int SD, int OD, bool EPI = false>
+template <class C, int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O, int64_t M,
-                           int64_t N, int64_t K, int64_t G, int splits, hipStream_t st) {
+                           int64_t N, int64_t K, int64_t G, int splits, hipStream_t st,
+                           int sd_rt = 0, int od_rt = 0) {
   const int tiles_m = int((M + C::BM - 1) / C::BM);
   const int tiles_n = int((N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm_w4_kernel<C, WBITS, SD, OD, EPI>), dim3(unsigned(tiles_m * tiles_n), unsigned(splits)),
+  hipLaunchKernelGGL((gemm_w4_kernel<C, WBITS, SD, OD, EPI, XD>), dim3(unsigned(tiles_m * tiles_n), unsigned(splits)),
                      dim3(C::kThreads), 0, st, static_cast<const half_t*>(X),
                      static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K), int(K / G),
-                     int(G), tiles_m, tiles_n, int(K / splits));
+                     int(G), tiles_m, tiles_n, int(K / splits), sd_rt, od_rt);
   return check_launch();
 }
 
@@ -496,19 +547,19 @@ int static_scratch(void** ptr) {
 template <int OD>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ P,
                                                            void* __restrict__ O, size_t mn,
-                                                           int splits) {
+                                                           int splits, int od_rt = 0) {
   const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i >= mn) return;
   if (i + 4 <= mn && (mn & 3) == 0) {
     float4_t a = *reinterpret_cast<const float4_t*>(P + i);
     for (int s = 1; s < splits; ++s) a += *reinterpret_cast<const float4_t*>(P + size_t(s) * mn + i);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) store_f32<OD>(O, i + e, a[e]);
+    for (int e = 0; e < 4; ++e) store_out<OD>(O, i + e, a[e], od_rt);
   } else {
     for (size_t e = i; e < i + 4 && e < mn; ++e) {
       float a = P[e];
       for (int s = 1; s < splits; ++s) a += P[size_t(s) * mn + e];
-      store_f32<OD>(O, e, a);
+      store_out<OD>(O, e, a, od_rt);
     }
   }
 }
@@ -516,9 +567,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // int8 stages the scale rows of every group a split touches in kGemmScaleFloats
 // of LDS (128 rows): the fewest splits (dividing the 64-k steps) that keep a
 // split's groups within that; 0 = none does.  int4 needs no staging.
-template <int WBITS>
+template <int WBITS, bool POST = WBITS == 8>
 static int min_splits(int64_t K, int64_t G) {
-  if (WBITS == 4) return 1;
+  if (!POST) return 1;
   static_assert(GemmDefault::BN == 128 && GemmSmall::BN == 128, "scale staging sized for 128 rows");
   const int64_t ksteps = K / kBK;
   for (int64_t s = 1; s <= ksteps && s <= 64; ++s) {
@@ -564,10 +615,10 @@ static int choose_splits(int64_t tiles, int64_t K, int need) {
   return need;
 }
 
-template <class C, int WBITS, int SD, int OD, bool EPI = false>
+template <class C, int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 static int launch_gemm_split(const void* X, const void* W, const void* S, void* O, int64_t M,
                              int64_t N, int64_t K, int64_t G, int splits, hipStream_t st,
-                             const FixedScratch* fixed) {
+                             const FixedScratch* fixed, int sd_rt = 0, int od_rt = 0) {
   const size_t mn = size_t(M) * size_t(N);
   const size_t ws_bytes = mn * sizeof(float) * size_t(splits);
   void* ws;
@@ -578,23 +629,24 @@ static int launch_gemm_split(const void* X, const void* W, const void* S, void* 
     ws = ws_bytes <= kSplitWsMax ? split_workspace(ws_bytes, st) : nullptr;
     if (ws == nullptr) return LQ_ERR_SHAPE;
   }
-  int rc = launch_gemm_cfg<C, WBITS, SD, LQ_F32>(X, W, S, ws, M, N, K, G, splits, st);
+  int rc = launch_gemm_cfg<C, WBITS, SD, LQ_F32, false, XD>(X, W, S, ws, M, N, K, G, splits, st,
+                                                           sd_rt);
   if (rc != LQ_OK) return rc;
   if constexpr (EPI)
     hipLaunchKernelGGL((split_reduce_silu_kernel<OD>), dim3(unsigned((mn / 2 + 255) / 256)), dim3(256),
                        0, st, static_cast<const float*>(ws), O, M, N, splits);
   else
     hipLaunchKernelGGL((split_reduce_kernel<OD>), dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, st,
-                       static_cast<const float*>(ws), O, mn, splits);
+                       static_cast<const float*>(ws), O, mn, splits, od_rt);
   return check_launch();
 }
 
 // LQ_ERR_SHAPE: no configuration applies (the caller takes another kernel).
-template <int WBITS, int SD, int OD, bool EPI = false>
+template <int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, hipStream_t st,
-                         const FixedScratch* fixed = nullptr) {
-  const int need = min_splits<WBITS>(K, G);
+                         const FixedScratch* fixed = nullptr, int sd_rt = 0, int od_rt = 0) {
+  const int need = min_splits<WBITS, WBITS == 8 || XD == LQ_BF16>(K, G);
   if (need == 0) return LQ_ERR_SHAPE;
   // 256-row tiles only when they alone give every CU (256) a tile; below that
   // (M <= 1024 at N = 4096) 128 x 128 tiles finish sooner, split over k when
@@ -602,23 +654,29 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
   const int64_t big_tiles = ((M + GemmDefault::BM - 1) / GemmDefault::BM) *
                             ((N + GemmDefault::BN - 1) / GemmDefault::BN);
   if (big_tiles >= 256) {
-    if (need == 1) return launch_gemm_cfg<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 1, st);
-    return launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, need, st, fixed);
+    if (need == 1)
+      return launch_gemm_cfg<GemmDefault, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G, 1, st,
+                                                                 sd_rt, od_rt);
+    return launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G, need, st,
+                                                                  fixed, sd_rt, od_rt);
   }
   // Half the CUs or more with 256-row tiles: those tiles with k split in two
   // beat twice as many 128-row tiles (M = 1024 at N = 4096: 62.7 -> 56.9 us).
   if (big_tiles >= 128 && need <= 2 && (K / kBK) % 2 == 0 && K / kBK >= 8) {
-    const int rc = launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 2, st, fixed);
+    const int rc = launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G, 2,
+                                                                          st, fixed, sd_rt, od_rt);
     if (rc != LQ_ERR_SHAPE || need > 1) return rc;
   }
   const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
                         ((N + GemmSmall::BN - 1) / GemmSmall::BN);
   const int splits = choose_splits(tiles, K, need);
   if (splits > 1) {
-    const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, splits, st, fixed);
+    const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G,
+                                                                        splits, st, fixed, sd_rt, od_rt);
     if (rc != LQ_ERR_SHAPE || need > 1) return rc;
   }
-  return launch_gemm_cfg<GemmSmall, WBITS, SD, OD, EPI>(X, W, S, O, M, N, K, G, 1, st);
+  return launch_gemm_cfg<GemmSmall, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G, 1, st, sd_rt,
+                                                           od_rt);
 }
 
 template <int WBITS>
@@ -664,6 +722,20 @@ int launch_gemm_silu(const void* X, const void* W, const void* S, void* O, int64
 #undef LQ_GS
   return LQ_ERR_SHAPE;
 }
+
+// bf16 activations: bf16 MFMAs on exact integer weights, fp32 group scales
+// (groups of whole 64-k steps); scale / output dtypes at run time.
+template <int WBITS>
+int launch_gemm_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                  int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st,
+                  const FixedScratch* fixed) {
+  if (xd != LQ_BF16 || G % kBK != 0) return LQ_ERR_SHAPE;
+  return launch_gemm_t<WBITS, kRT, kRT, false, LQ_BF16>(X, W, S, O, M, N, K, G, st, fixed, sd, od);
+}
+template int launch_gemm_x<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
+                              int64_t, int64_t, int, int, int, hipStream_t, const FixedScratch*);
+template int launch_gemm_x<8>(const void*, const void*, const void*, void*, int64_t, int64_t,
+                              int64_t, int64_t, int, int, int, hipStream_t, const FixedScratch*);
 
 template int launch_gemm<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
                             int64_t, int64_t, int, int, hipStream_t, const FixedScratch*);

@@ -721,6 +721,173 @@ __global__ __launch_bounds__(256, 2) void gemv_diag_kernel(
 }
 
 
+// MFMA operand traits of the tile kernels, by weight bits and activation
+// dtype XD.  kSpan = k per MFMA block (one weight dword per lane), kXLoads =
+// 16-byte activation loads per lane per block, kMagic = the OR mask of the
+// biased weight decode.  fp16 activations feed fp16 MFMAs.  bf16 activations
+// feed bf16 MFMAs with exact integer weights: int4 as bf16 128 + q
+// (0x4300 | q), int8 as 128 + q via an exact byte -> float conversion, the
+// bias removed by a bias chain and the scale applied in fp32 per group.
+// fp32 activations are split exactly into three bf16 parts, x = hi + mid +
+// lo (hi = x truncated to bf16, mid = the residual truncated, lo = the rest,
+// which has at most 8 significant bits), fed as separate MFMA rows
+// (m + 4 part) whose sums are added in fp32: every product of a part and an
+// integer weight is exact in fp32.
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+typedef short s4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
+template <int WBITS, int XD = LQ_F16> struct TileMfma;
+template <> struct TileMfma<4, LQ_F16> {
+  static constexpr int kSpan = 32;      // k per MFMA block (one dword of int4)
+  static constexpr int kXLoads = 1;
+  static constexpr uint32_t kMagic = 0x64006400u;
+  static constexpr bool kBiased = true;
+  typedef h8 op_t;
+  typedef u32x4_t x_t;                  // 8 activations per lane per block
+  // (k0, k4) (k1, k5) (k2, k6) (k3, k7) as 1024 + q, 1024 + 16 q, 1024 + q, 1024 + 16 q
+  __device__ static op_t decode(uint32_t w, uint32_t magic) {
+    const uint32_t w8 = w >> 8;
+    u32x4_t b;
+    b.x = and_or(w, 0x000F000Fu, magic);
+    b.y = and_or(w, 0x00F000F0u, magic);
+    b.z = and_or(w8, 0x000F000Fu, magic);
+    b.w = and_or(w8, 0x00F000F0u, magic);
+    return __builtin_bit_cast(h8, b);
+  }
+  // activations in the same order, the 16 q slots divided by 16 (exact)
+  __device__ static op_t prep_x(const x_t& x, int = 0) {
+    const half2_t sixteenth = {half_t(0.0625f), half_t(0.0625f)};
+    u32x4_t v = xperm8(x);
+    v.y = as_u32(as_h2(v.y) * sixteenth);
+    v.w = as_u32(as_h2(v.w) * sixteenth);
+    return __builtin_bit_cast(h8, v);
+  }
+  // -(bias) per slot: x * (1024 + q) - 1032 x = x (q - 8); (x / 16)(1024 + 16 q) - 1152 (x / 16) = x (q - 8)
+  __device__ static op_t neg_bias() {
+    const half2_t a = {half_t(-1032.f), half_t(-1032.f)};
+    const half2_t b = {half_t(-1152.f), half_t(-1152.f)};
+    u32x4_t v;
+    v.x = as_u32(a); v.y = as_u32(b); v.z = as_u32(a); v.w = as_u32(b);
+    return __builtin_bit_cast(h8, v);
+  }
+  __device__ static float4_t mfma(const op_t& a, const op_t& b, const float4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+template <> struct TileMfma<8, LQ_F16> {
+  static constexpr int kSpan = 16;      // k per MFMA block (one dword of int8)
+  static constexpr int kXLoads = 1;
+  static constexpr uint32_t kMagic = 0x64006400u;
+  static constexpr bool kBiased = false;
+  typedef h4 op_t;
+  typedef u32x2_t x_t;                  // 4 activations per lane per block
+  __device__ static op_t decode(uint32_t w, uint32_t) {
+    half2_t hb[2];
+    int8x4_to_h2(w, hb);
+    h4 r;
+    r[0] = hb[0][0]; r[1] = hb[0][1]; r[2] = hb[1][0]; r[3] = hb[1][1];
+    return r;
+  }
+  __device__ static op_t prep_x(const x_t& x, int = 0) { return __builtin_bit_cast(h4, x); }
+  __device__ static op_t neg_bias() { return op_t{}; }
+  __device__ static float4_t mfma(const op_t& a, const op_t& b, const float4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// int4 -> bf16 pairs (k_i, k_{i+4}) = 128 + q: nibble i of bytes 0 and 2.
+__device__ __forceinline__ u32x4_t int4x8_bf16_biased(uint32_t w, uint32_t magic) {
+  return int4x8_biased_kperm_m(w, magic);
+}
+// int8 -> four bf16 128 + q, k order kept (u = q ^ 0x80 = q + 128 is exact as
+// a float and as bf16: at most 8 significant bits, so the float's low half is 0).
+__device__ __forceinline__ u32x2_t int8x4_bf16_biased(uint32_t w) {
+  const uint32_t u = w ^ 0x80808080u;
+  const float f0 = float(u & 0xFFu), f1 = float((u >> 8) & 0xFFu);
+  const float f2 = float((u >> 16) & 0xFFu), f3 = float(u >> 24);
+  u32x2_t r;
+  r.x = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+  r.y = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+  return r;
+}
+// Part `part` (0 hi, 1 mid, 2 lo) of the exact 3-way bf16 split of fp32 x,
+// as the bf16 bit pattern in the high half of the returned dword.
+__device__ __forceinline__ uint32_t f32_part_bits(uint32_t x, int part) {
+  const uint32_t hi = x & 0xFFFF0000u;
+  const float r1 = __uint_as_float(x) - __uint_as_float(hi);
+  const uint32_t mid = __float_as_uint(r1) & 0xFFFF0000u;
+  const float r2 = r1 - __uint_as_float(mid);
+  return part == 0 ? hi : part == 1 ? mid : __float_as_uint(r2);
+}
+
+template <> struct TileMfma<4, LQ_BF16> {
+  static constexpr int kSpan = 32;
+  static constexpr int kXLoads = 1;
+  static constexpr uint32_t kMagic = 0x43004300u;
+  static constexpr bool kBiased = true;
+  typedef bf8_t op_t;
+  typedef u32x4_t x_t;
+  __device__ static op_t decode(uint32_t w, uint32_t magic) {
+    return __builtin_bit_cast(bf8_t, int4x8_bf16_biased(w, magic));
+  }
+  __device__ static op_t prep_x(const x_t& x, int = 0) { return __builtin_bit_cast(bf8_t, xperm8(x)); }
+  __device__ static op_t neg_bias() {   // -136 = -(128 + 8)
+    const u32x4_t v = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
+    return __builtin_bit_cast(bf8_t, v);
+  }
+  __device__ static float4_t mfma(const op_t& a, const op_t& b, const float4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct TileMfma<8, LQ_BF16> {
+  static constexpr int kSpan = 16;
+  static constexpr int kXLoads = 1;
+  static constexpr uint32_t kMagic = 0;
+  static constexpr bool kBiased = true;
+  typedef s4_t op_t;
+  typedef u32x2_t x_t;
+  __device__ static op_t decode(uint32_t w, uint32_t) {
+    return __builtin_bit_cast(s4_t, int8x4_bf16_biased(w));
+  }
+  __device__ static op_t prep_x(const x_t& x, int = 0) { return __builtin_bit_cast(s4_t, x); }
+  __device__ static op_t neg_bias() {   // -128
+    const u32x2_t v = {0xC300C300u, 0xC300C300u};
+    return __builtin_bit_cast(s4_t, v);
+  }
+  __device__ static float4_t mfma(const op_t& a, const op_t& b, const float4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct TileMfma<4, LQ_F32> : TileMfma<4, LQ_BF16> {
+  static constexpr int kXLoads = 2;
+  typedef u32x8_t x_t;
+  // 8 fp32 activations -> part `part` as bf16 in the decode's k order
+  __device__ static op_t prep_x(const x_t& x, int part) {
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = f32_part_bits(x[i], part);
+    u32x4_t v;
+    v.x = __builtin_amdgcn_perm(b[4], b[0], 0x07060302u);
+    v.y = __builtin_amdgcn_perm(b[5], b[1], 0x07060302u);
+    v.z = __builtin_amdgcn_perm(b[6], b[2], 0x07060302u);
+    v.w = __builtin_amdgcn_perm(b[7], b[3], 0x07060302u);
+    return __builtin_bit_cast(bf8_t, v);
+  }
+};
+template <> struct TileMfma<8, LQ_F32> : TileMfma<8, LQ_BF16> {
+  typedef u32x4_t x_t;
+  __device__ static op_t prep_x(const x_t& x, int part) {
+    uint32_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = f32_part_bits(x[i], part);
+    u32x2_t v;
+    v.x = __builtin_amdgcn_perm(b[1], b[0], 0x07060302u);
+    v.y = __builtin_amdgcn_perm(b[3], b[2], 0x07060302u);
+    return __builtin_bit_cast(s4_t, v);
+  }
+};
+
 // --------------------------- decode GEMV, MFMA diagonal, 2048-k segments --
 // Same scheme as gemv_diag_kernel with the overhead removed:
 //   * buffer loads (SGPR resource, 32-bit lane offsets, row offset in the
@@ -737,11 +904,20 @@ __global__ __launch_bounds__(256, 2) void gemv_diag_kernel(
 // lane offset past every buffer's end (sizes < 2^31 - 2^30 are checked on the host)
 constexpr int kSegOob = 0x40000000;
 
-template <int M_, int NSEG, int RW, int SD, int OD, bool PART>
+// XD: activation dtype.  bf16 / fp32 activations run bf16 MFMAs on weights
+// decoded to bf16 128 + q (0x4300 | q, 7 VALU ops per dword); fp32 ones as
+// three exact bf16 parts (hi + mid + lo) whose MFMAs chain into the same
+// accumulator.  SD / OD = kRT take the dtypes from sd_rt / od_rt.
+template <int M_, int NSEG, int RW, int SD, int OD, bool PART, int XD = LQ_F16>
 __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
-    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
-    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
-  typedef typename Elem<SD>::T stype;
+    const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
+    int od_rt = 0) {
+  constexpr bool kH = XD == LQ_F16;
+  constexpr int NP = XD == LQ_F32 ? 3 : 1;     // bf16 parts per activation
+  constexpr int kXB = XD == LQ_F32 ? 4 : 2;    // activation element bytes
+  const int sd = SD == kRT ? sd_rt : SD;
+  const int ssz = sd == LQ_F32 ? 4 : 2;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * 4 + wave) * RW;
@@ -751,15 +927,15 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   const bool diag = q == (j >> 2);
   const int dreg = j & 3;
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<half_t*>(X), 0, M * K * 2, 0x00020000);
+      const_cast<void*>(X), 0, M * K * kXB, 0x00020000);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(W), 0, N * half_k, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<void*>(S), 0, N * num_scales * int(sizeof(stype)), 0x00020000);
+      const_cast<void*>(S), 0, N * num_scales * ssz, 0x00020000);
 
   // 1. activations (rows m >= M read as zeros): thread t fetches the chunk
   // lane t / 4 of every wave uses as its operand e = t % 4
-  u32x4_t xv2[M_][NSEG];
+  u32x4_t xv2[M_][NSEG][kXB / 2];   // 8 activations: one (2-byte) or two (fp32) loads
   {
     const int tl = threadIdx.x >> 2, te = threadIdx.x & 3;
     const int tpos = 4 * (tl & 15) + (tl >> 4);
@@ -767,9 +943,12 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
     for (int m = 0; m < M_; ++m)
 #pragma unroll
       for (int c = 0; c < NSEG; ++c)
-        xv2[m][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-            rx, !PART || c * 2048 + tpos * 32 < K ? (m * K + c * 2048 + tpos * 32 + te * 8) * 2 : kSegOob,
-            0, 0));
+#pragma unroll
+        for (int h = 0; h < kXB / 2; ++h)
+          xv2[m][c][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+              rx, !PART || c * 2048 + tpos * 32 < K ? (m * K + c * 2048 + tpos * 32 + te * 8) * kXB + 16 * h
+                                                    : kSegOob,
+              0, 0));
   }
   // 2. scales
   uint32_t sv[RW][NSEG];
@@ -779,7 +958,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
     for (int c = 0; c < NSEG; ++c) {
       const bool kin = !PART || c * 2048 + pos * 32 < K;
       const int g = (c * 2048 + pos * 32) / group;
-      if constexpr (sizeof(stype) == 2)
+      if (ssz == 2)
         sv[r][c] = __builtin_amdgcn_raw_buffer_load_b16(rs, kin ? g * 2 : kSegOob, ((n0 + r) * num_scales) * 2, 0);
       else
         sv[r][c] = __builtin_amdgcn_raw_buffer_load_b32(rs, kin ? g * 4 : kSegOob, ((n0 + r) * num_scales) * 4, 0);
@@ -800,7 +979,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   // in LDS: every thread converts M_ * NSEG of the 16-byte chunks (chunk
   // (m, c, lane, e) -> slot), then waves 0.. compute -bias for one (m, c)
   // each with 4 MFMAs, then every wave reads its operands back.
-  __shared__ u32x4_t xs_l[M_ * NSEG * 256];
+  __shared__ u32x4_t xs_l[M_ * NSEG * NP * 256];
   __shared__ float4_t nc_l[M_ * NSEG * 64];
   const half2_t sixteenth = {half_t(0.0625f), half_t(0.0625f)};
   {
@@ -810,42 +989,66 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 #pragma unroll
       for (int c = 0; c < NSEG; ++c) {
         // thread t converts the chunk that lane t / 4 uses as its e = t % 4 operand
-        u32x4_t v = xperm8(xv2[m][c]);
-        v.y = as_u32(as_h2(v.y) * sixteenth);
-        v.w = as_u32(as_h2(v.w) * sixteenth);
-        xs_l[(m * NSEG + c) * 256 + t] = v;
+        if constexpr (kH) {
+          u32x4_t v = xperm8(xv2[m][c][0]);
+          v.y = as_u32(as_h2(v.y) * sixteenth);
+          v.w = as_u32(as_h2(v.w) * sixteenth);
+          xs_l[(m * NSEG + c) * 256 + t] = v;
+        } else if constexpr (XD == LQ_BF16) {
+          xs_l[(m * NSEG + c) * 256 + t] = xperm8(xv2[m][c][0]);
+        } else {
+          const u32x8_t x8 = {xv2[m][c][0].x, xv2[m][c][0].y, xv2[m][c][0].z, xv2[m][c][0].w,
+                              xv2[m][c][1].x, xv2[m][c][1].y, xv2[m][c][1].z, xv2[m][c][1].w};
+#pragma unroll
+          for (int p = 0; p < NP; ++p)
+            xs_l[((m * NSEG + c) * NP + p) * 256 + t] =
+                __builtin_bit_cast(u32x4_t, TileMfma<4, LQ_F32>::prep_x(x8, p));
+        }
       }
   }
   __syncthreads();
   {
-    const half2_t b1032 = {half_t(1032.f), half_t(1032.f)};
-    const half2_t b1152 = {half_t(1152.f), half_t(1152.f)};
-    u32x4_t bias_w;
-    bias_w.x = as_u32(b1032); bias_w.y = as_u32(b1152); bias_w.z = as_u32(b1032); bias_w.w = as_u32(b1152);
-    const h8 bias_op = __builtin_bit_cast(h8, bias_w);
     for (int mc = wave; mc < M_ * NSEG; mc += 4) {
       float4_t cr = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (kH) {
+        const half2_t b1032 = {half_t(1032.f), half_t(1032.f)};
+        const half2_t b1152 = {half_t(1152.f), half_t(1152.f)};
+        u32x4_t bias_w;
+        bias_w.x = as_u32(b1032); bias_w.y = as_u32(b1152); bias_w.z = as_u32(b1032); bias_w.w = as_u32(b1152);
+        const h8 bias_op = __builtin_bit_cast(h8, bias_w);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(h8, xs_l[mc * 256 + lane * 4 + e]), bias_op, cr, 0, 0, 0);
+        for (int e = 0; e < 4; ++e)
+          cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(h8, xs_l[mc * 256 + lane * 4 + e]), bias_op, cr, 0, 0, 0);
+      } else {
+        const u32x4_t b136 = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};   // 128 + 8
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            cr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf8_t, xs_l[(mc * NP + p) * 256 + lane * 4 + e]),
+                __builtin_bit_cast(bf8_t, b136), cr, 0, 0, 0);
+      }
       nc_l[mc * 64 + lane] = -cr;
     }
   }
   __syncthreads();
-  u32x4_t xv[M_][NSEG][4];
+  u32x4_t xv[M_][NSEG][NP][4];
   float4_t negcorr[M_][NSEG];
 #pragma unroll
   for (int m = 0; m < M_; ++m)
 #pragma unroll
     for (int c = 0; c < NSEG; ++c) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) xv[m][c][e] = xs_l[(m * NSEG + c) * 256 + lane * 4 + e];
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[m][c][p][e] = xs_l[((m * NSEG + c) * NP + p) * 256 + lane * 4 + e];
       negcorr[m][c] = nc_l[(m * NSEG + c) * 64 + lane];
     }
 
   // 5. rows: decode (5 ops / 8 weights) + MFMA, chains start at -bias
-  const uint32_t magic = opaque_u32(0x64006400u);
+  const uint32_t magic = opaque_u32(kH ? 0x64006400u : 0x43004300u);
   float acc[M_][RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
@@ -859,21 +1062,31 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t w = wv[r][c][e];
-        const uint32_t w8 = w >> 8;
-        u32x4_t b;
-        b.x = and_or(w, 0x000F000Fu, magic);
-        b.y = and_or(w, 0x00F000F0u, magic);
-        b.z = and_or(w8, 0x000F000Fu, magic);
-        b.w = and_or(w8, 0x00F000F0u, magic);
-        const h8 bop = __builtin_bit_cast(h8, b);
+        if constexpr (kH) {
+          const uint32_t w8 = w >> 8;
+          u32x4_t b;
+          b.x = and_or(w, 0x000F000Fu, magic);
+          b.y = and_or(w, 0x00F000F0u, magic);
+          b.z = and_or(w8, 0x000F000Fu, magic);
+          b.w = and_or(w8, 0x00F000F0u, magic);
+          const h8 bop = __builtin_bit_cast(h8, b);
 #pragma unroll
-        for (int m = 0; m < M_; ++m)
-          d[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xv[m][c][e]), bop,
-                                                        d[m], 0, 0, 0);
+          for (int m = 0; m < M_; ++m)
+            d[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xv[m][c][0][e]),
+                                                          bop, d[m], 0, 0, 0);
+        } else {
+          const bf8_t bop = __builtin_bit_cast(bf8_t, int4x8_biased_kperm_m(w, magic));
+#pragma unroll
+          for (int m = 0; m < M_; ++m)
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+              d[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8_t, xv[m][c][p][e]),
+                                                             bop, d[m], 0, 0, 0);
+        }
       }
       float sc;
-      if constexpr (SD == LQ_F32) sc = __uint_as_float(sv[r][c]);
-      else if constexpr (SD == LQ_F16) sc = float(__builtin_bit_cast(half_t, uint16_t(sv[r][c])));
+      if (sd == LQ_F32) sc = __uint_as_float(sv[r][c]);
+      else if (sd == LQ_F16) sc = float(__builtin_bit_cast(half_t, uint16_t(sv[r][c])));
       else sc = bf16_to_f32(uint16_t(sv[r][c]));
 #pragma unroll
       for (int m = 0; m < M_; ++m) {
@@ -911,7 +1124,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
       for (int c2 = RW; c2 > 1; c2 >>= 1, w2 >>= 1) row = row * 2 + ((lane & w2) ? 1 : 0);
     }
     const int lowmask = (64 / RW) - 1;
-    if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+    if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_out<OD>(O, size_t(m) * N + n0 + row, v[0], od_rt);
   }
 }
 
@@ -944,62 +1157,6 @@ constexpr int kTSlots = 4;
 constexpr int kTWaves = 8;
 constexpr int kTBlocks = 4;             // MFMA blocks per wave per chunk
 
-template <int WBITS> struct TileMfma;
-template <> struct TileMfma<4> {
-  static constexpr int kSpan = 32;      // k per MFMA block (one dword of int4)
-  static constexpr bool kBiased = true;
-  typedef h8 op_t;
-  typedef u32x4_t x_t;                  // 8 activations per lane per block
-  // (k0, k4) (k1, k5) (k2, k6) (k3, k7) as 1024 + q, 1024 + 16 q, 1024 + q, 1024 + 16 q
-  __device__ static op_t decode(uint32_t w, uint32_t magic) {
-    const uint32_t w8 = w >> 8;
-    u32x4_t b;
-    b.x = and_or(w, 0x000F000Fu, magic);
-    b.y = and_or(w, 0x00F000F0u, magic);
-    b.z = and_or(w8, 0x000F000Fu, magic);
-    b.w = and_or(w8, 0x00F000F0u, magic);
-    return __builtin_bit_cast(h8, b);
-  }
-  // activations in the same order, the 16 q slots divided by 16 (exact)
-  __device__ static op_t prep_x(const x_t& x) {
-    const half2_t sixteenth = {half_t(0.0625f), half_t(0.0625f)};
-    u32x4_t v = xperm8(x);
-    v.y = as_u32(as_h2(v.y) * sixteenth);
-    v.w = as_u32(as_h2(v.w) * sixteenth);
-    return __builtin_bit_cast(h8, v);
-  }
-  // -(bias) per slot: x * (1024 + q) - 1032 x = x (q - 8); (x / 16)(1024 + 16 q) - 1152 (x / 16) = x (q - 8)
-  __device__ static op_t neg_bias() {
-    const half2_t a = {half_t(-1032.f), half_t(-1032.f)};
-    const half2_t b = {half_t(-1152.f), half_t(-1152.f)};
-    u32x4_t v;
-    v.x = as_u32(a); v.y = as_u32(b); v.z = as_u32(a); v.w = as_u32(b);
-    return __builtin_bit_cast(h8, v);
-  }
-  __device__ static float4_t mfma(const op_t& a, const op_t& b, const float4_t& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-template <> struct TileMfma<8> {
-  static constexpr int kSpan = 16;      // k per MFMA block (one dword of int8)
-  static constexpr bool kBiased = false;
-  typedef h4 op_t;
-  typedef u32x2_t x_t;                  // 4 activations per lane per block
-  __device__ static op_t decode(uint32_t w, uint32_t) {
-    half2_t hb[2];
-    int8x4_to_h2(w, hb);
-    h4 r;
-    r[0] = hb[0][0]; r[1] = hb[0][1]; r[2] = hb[1][0]; r[3] = hb[1][1];
-    return r;
-  }
-  __device__ static op_t prep_x(const x_t& x) { return __builtin_bit_cast(h4, x); }
-  __device__ static op_t neg_bias() { return op_t{}; }
-  __device__ static float4_t mfma(const op_t& a, const op_t& b, const float4_t& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-  }
-};
-
 constexpr int kTScaleLds = 32 * 1024;  // LDS for one workgroup's scale rows
 
 // Copies 16 bytes per lane from a raw buffer (offset voff) to LDS (lane L ->
@@ -1015,18 +1172,25 @@ __device__ __forceinline__ void dma16_buf(i32x4_t rsrc, uint32_t voff, const voi
 // a partial chunk (the masked path below; whole-chunk rows skip its cost);
 // EPI = gate/up rows interleaved (2i, 2i + 1): store silu(gate) * up to
 // O [M, N / 2] instead of O [M, N].
-template <int WBITS, int NSC, int TILES, int SD, int OD, bool PART, bool EPI = false>
+// XD = activation dtype (fp16, bf16, or fp32 for M <= 4: MFMA row
+// m + 4 part holds part `part` of activation row m); SD / OD = kRT take the
+// scale / output dtype from sd_rt / od_rt.
+template <int WBITS, int NSC, int TILES, int SD, int OD, bool PART, bool EPI = false,
+          int XD = LQ_F16>
 __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
-    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
-    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
-  typedef TileMfma<WBITS> Mf;
+    const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
+    int od_rt = 0) {
+  typedef TileMfma<WBITS, XD> Mf;
   typedef typename Mf::op_t op_t;
   typedef typename Mf::x_t x_t;
   constexpr int kSpan = Mf::kSpan;                      // k per MFMA block
   constexpr int kEighthK = kTBlocks * kSpan;            // k per wave per chunk
   constexpr int kChunkK = kTWaves * kEighthK;
   constexpr int kPerScale = kTBlocks / NSC;             // blocks sharing one scale
-  constexpr int kSSize = SD == LQ_F32 ? 4 : 2;
+  constexpr int kXB = XD == LQ_F32 ? 4 : 2;             // activation element bytes
+  constexpr bool kSplit = XD == LQ_F32;
+  const int kSSize = scale_size<SD>(sd_rt);
   constexpr int kRows = 16 * TILES;
   constexpr int kDma = TILES;                           // DMA instructions per wave per chunk
   constexpr int kSlotB = kRows * kTChunkB;
@@ -1084,14 +1248,18 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   };
 
   // Lane (m = r16, q4) supplies activation row m, k = block * kSpan + q4 * kSpan / 4 + 0 ..
-  const half_t* xrow = X + size_t(min(r16, M - 1)) * K + wave * kEighthK + q4 * (kSpan / 4);
+  // (fp32: MFMA row r16 = m + 4 part, m = r16 % 4)
+  const int xm = kSplit ? (r16 & 3) : r16;
+  const int xpart = kSplit ? (r16 >> 2) : 0;
+  const uint8_t* xrow = static_cast<const uint8_t*>(X) +
+                        (size_t(min(xm, M - 1)) * K + wave * kEighthK + q4 * (kSpan / 4)) * kXB;
   struct Batch {
     x_t x[kTBlocks];
   };
-  // Lanes of activation rows m >= M load nothing (their registers hold
-  // whatever they held): MFMA rows are independent and rows m >= M are never
-  // stored, so this only saves requests.
-  const bool x_lane = r16 < M;
+  // Lanes of activation rows m >= M (and fp32 part 3) load nothing (their
+  // registers hold whatever they held): MFMA rows are independent and those
+  // rows are never stored, so this only saves requests.
+  const bool x_lane = xm < M && xpart < 3;
   auto load_batch = [&](Batch& bt, int c) {
     const int ch = phys(c);
     if (!x_lane) return;
@@ -1099,8 +1267,12 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
 #pragma unroll
     for (int f = 0; f < kTBlocks; ++f) {
       // past K (partial last chunk): load from the row start, zeroed in compute()
-      const half_t* px = !PART || k0 + f * kSpan < K ? xrow + ch * kChunkK + f * kSpan : X;
-      if constexpr (sizeof(x_t) == 16) {
+      const uint8_t* px = !PART || k0 + f * kSpan < K ? xrow + size_t(ch * kChunkK + f * kSpan) * kXB
+                                                       : static_cast<const uint8_t*>(X);
+      if constexpr (sizeof(x_t) == 32) {
+        u32x4_t a = gload_b128_cached(px), b = gload_b128_cached(px + 16);
+        bt.x[f] = u32x8_t{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      } else if constexpr (sizeof(x_t) == 16) {
         bt.x[f] = gload_b128_cached(px);
       } else {
         __asm__ volatile("global_load_dwordx2 %0, %1, off" : "=v"(bt.x[f]) : "v"(px) : "memory");
@@ -1110,7 +1282,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   // A group = everything chunk c needs: its activation/scale batch and its
   // weight DMA.  Name the batch registers after the wait that covers them so
   // nothing reads them early.
-  constexpr int kGroupLoads = kTBlocks + kDma;
+  constexpr int kGroupLoads = kTBlocks * Mf::kXLoads + kDma;
   auto tie_batch = [&](Batch& bt) {
 #pragma unroll
     for (int f = 0; f < kTBlocks; ++f) __asm__ volatile("" : "+v"(bt.x[f]));
@@ -1128,7 +1300,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
     dma_chunk(c & 3, c);
   };
 
-  const uint32_t magic = opaque_u32(0x64006400u);
+  const uint32_t magic = opaque_u32(Mf::kMagic);
   float4_t acc[TILES];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -1154,16 +1326,13 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
       for (int sg = 0; sg < NSC; ++sg) {
         int g = (kbase + sg * kPerScale * kSpan) / group;
         if constexpr (PART) g = min(g, num_scales - 1);
-        const uint8_t* ps = sl + (size_t(row) * num_scales + g) * kSSize;
-        if constexpr (SD == LQ_F32) sc[t][sg] = *reinterpret_cast<const float*>(ps);
-        else if constexpr (SD == LQ_F16) sc[t][sg] = float(*reinterpret_cast<const half_t*>(ps));
-        else sc[t][sg] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
+        sc[t][sg] = load_scale<SD>(sl + (size_t(row) * num_scales + g) * kSSize, sd_rt);
       }
     }
     op_t xa[kTBlocks];
 #pragma unroll
     for (int f = 0; f < kTBlocks; ++f) {
-      xa[f] = Mf::prep_x(bt.x[f]);
+      xa[f] = Mf::prep_x(bt.x[f], xpart);
       if (PART && kbase + f * kSpan + q4 * (kSpan / 4) >= K) xa[f] = op_t{};
     }
 #pragma unroll
@@ -1247,17 +1416,29 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
 #pragma unroll
     for (int w = 1; w < kTWaves; ++w) v += red[(w * TILES + t) * 64 + lane];
     const int n = n0 + t * 16 + r16;
+    if constexpr (kSplit) {
+      // activation row m's three parts: MFMA rows m, m + 4, m + 8 = register
+      // m of lanes r16, r16 + 16, r16 + 32
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = q4 * 4 + r;
-      if constexpr (EPI) {
-        // rows 2i (gate) and 2i + 1 (up) sit in lanes r16 and r16 ^ 1
-        const float up = __shfl_xor(v[r], 1, 64);
-        const float g = v[r];
-        if ((r16 & 1) == 0 && m < M && n < N)
-          store_f32<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up);
-      } else {
-        if (m < M && n < N) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+      for (int r = 0; r < 4; ++r) v[r] += __shfl(v[r], lane + 16, 64) + __shfl(v[r], lane + 32, 64);
+      if (q4 == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (r < M && n < N) store_out<OD>(O, size_t(r) * N + n, v[r], od_rt);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = q4 * 4 + r;
+        if constexpr (EPI) {
+          // rows 2i (gate) and 2i + 1 (up) sit in lanes r16 and r16 ^ 1
+          const float up = __shfl_xor(v[r], 1, 64);
+          const float g = v[r];
+          if ((r16 & 1) == 0 && m < M && n < N)
+            store_out<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up, od_rt);
+        } else {
+          if (m < M && n < N) store_out<OD>(O, size_t(m) * N + n, v[r], od_rt);
+        }
       }
     }
   }
@@ -1848,7 +2029,8 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
 
 // Gate|up GEMV with the SiLU * mul epilogue on the row-contiguous kernel
 // (int4, M <= 2, G % 32 == 0).  Returns LQ_ERR_SHAPE when it does not apply.
-inline int launch_rows_silu(const void* X, const void* W, const void* S, void* O, int64_t M,
+template <int WBITS_ = 4>   // a template so that only the TUs that call it instantiate its kernels
+int launch_rows_silu(const void* X, const void* W, const void* S, void* O, int64_t M,
                             int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
   // 16 < M <= 64: the activation-in-LDS kernel with the same epilogue
   if (gemv_tile_xl_ok(4, M, N, K, G, sd == LQ_F32 ? 4 : 2)) {

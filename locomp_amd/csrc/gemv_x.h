@@ -1,0 +1,102 @@
+// Decode (M <= 16) dequant-matmul for bf16 and fp32 activations: the LDS-ring
+// tile kernel of gemv_impl.h instantiated with bf16 MFMAs (TileMfma<WBITS,
+// LQ_BF16 / LQ_F32>), scale and output dtypes taken at run time.
+#pragma once
+#include "gemv_impl.h"
+
+namespace lq {
+
+template <int WBITS, int XD, int NSC>
+static void launch_tile_x_nsc(const void* X, const void* W, const void* S, void* O, int64_t M,
+                              int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  // fp32 activations hold twice the registers per batch: at most 2 tiles
+  // (3 and 4 spill)
+  int tiles = gemv_tile_count(N, K, G, sd == LQ_F32 ? 4 : 2);
+  if (XD == LQ_F32 && tiles > 2) tiles = 2;
+  const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
+  const bool part = ((WBITS == 4 ? K / 2 : K) % kTChunkB) != 0;
+#define LQ_TX_LAUNCH(T_)                                                                        \
+  do {                                                                                          \
+    if (part)                                                                                   \
+      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, kRT, kRT, true, false, XD>),         \
+                         dim3(blocks), dim3(512), 0, st, X, static_cast<const uint8_t*>(W), S, \
+                         O, int(M), int(N), int(K), int(K / G), int(G), sd, od);                \
+    else                                                                                        \
+      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, kRT, kRT, false, false, XD>),        \
+                         dim3(blocks), dim3(512), 0, st, X, static_cast<const uint8_t*>(W), S, \
+                         O, int(M), int(N), int(K), int(K / G), int(G), sd, od);                \
+  } while (0)
+  if constexpr (XD == LQ_F32) {
+    if (tiles == 1) LQ_TX_LAUNCH(1);
+    else LQ_TX_LAUNCH(2);
+  } else {
+    switch (tiles) {
+      case 1: LQ_TX_LAUNCH(1); break;
+      case 2: LQ_TX_LAUNCH(2); break;
+      case 3: LQ_TX_LAUNCH(3); break;
+      default: LQ_TX_LAUNCH(4); break;
+    }
+  }
+#undef LQ_TX_LAUNCH
+}
+
+template <int NSEG, int RW, int XD>
+static void launch_seg_x_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                           int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  const unsigned blocks = unsigned((N + 4 * RW - 1) / (4 * RW));
+  if (K % 2048)
+    hipLaunchKernelGGL((gemv_seg_kernel<1, NSEG, RW, kRT, kRT, true, XD>), dim3(blocks), dim3(256), 0,
+                       st, X, static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K),
+                       int(K / G), int(G), sd, od);
+  else
+    hipLaunchKernelGGL((gemv_seg_kernel<1, NSEG, RW, kRT, kRT, false, XD>), dim3(blocks), dim3(256), 0,
+                       st, X, static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K),
+                       int(K / G), int(G), sd, od);
+}
+
+// M = 1, int4, G % 128: the 2048-k segment kernel (bf16 up to 8 segments,
+// fp32 - three operand sets per segment - up to 2); LQ_ERR_SHAPE otherwise.
+static int launch_seg_x(const void* X, const void* W, const void* S, void* O, int64_t M,
+                        int64_t N, int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
+  const int64_t nseg = (K + 2047) / 2048;
+  if (M != 1 || !gemv_seg_ok(4, 1, N, K, G)) return LQ_ERR_SHAPE;
+  if (xd == LQ_BF16) {
+    if (nseg == 1) launch_seg_x_t<1, 8, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+    else if (nseg == 2) launch_seg_x_t<2, 4, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+    else if (nseg <= 4) launch_seg_x_t<4, 2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+    else launch_seg_x_t<8, 1, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+  } else {
+    if (nseg == 1) launch_seg_x_t<1, 4, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
+    else if (nseg == 2) launch_seg_x_t<2, 2, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
+    else return LQ_ERR_SHAPE;
+  }
+  return check_launch();
+}
+
+// bf16 activations at M <= 16, fp32 at M <= 4 (three MFMA rows per
+// activation row), on the shapes gemv_tile_ok accepts; LQ_ERR_SHAPE otherwise.
+// int4 M = 1 with G % 128 takes the segment kernel.
+template <int WBITS>
+int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                    int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
+  if (xd != LQ_BF16 && xd != LQ_F32) return LQ_ERR_SHAPE;
+  if constexpr (WBITS == 4) {
+    const int rc = launch_seg_x(X, W, S, O, M, N, K, G, xd, sd, od, st);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
+  if (xd == LQ_F32 ? M > 4 : M > 16) return LQ_ERR_SHAPE;
+  if (!gemv_tile_ok(WBITS, M, N, K, G, sd == LQ_F32 ? 4 : 2)) return LQ_ERR_SHAPE;
+  const int64_t eighth_k = kTBlocks * TileMfma<WBITS>::kSpan;
+  const int nsc = G >= eighth_k ? 1 : int(eighth_k / G);
+#define LQ_NSC(XD_)                                                                         \
+  switch (nsc) {                                                                            \
+    case 1: launch_tile_x_nsc<WBITS, XD_, 1>(X, W, S, O, M, N, K, G, sd, od, st); break;    \
+    case 2: launch_tile_x_nsc<WBITS, XD_, 2>(X, W, S, O, M, N, K, G, sd, od, st); break;    \
+    default: launch_tile_x_nsc<WBITS, XD_, 4>(X, W, S, O, M, N, K, G, sd, od, st); break;   \
+  }
+  if (xd == LQ_BF16) { LQ_NSC(LQ_BF16) } else { LQ_NSC(LQ_F32) }
+#undef LQ_NSC
+  return check_launch();
+}
+
+}  // namespace lq

@@ -1,0 +1,7 @@
+// bf16 / fp32-activation decode kernels for int4 weights; see gemv_x.h.
+#include "gemv_x.h"
+
+namespace lq {
+template int launch_skinny_x<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
+                                int64_t, int64_t, int, int, int, hipStream_t);
+}  // namespace lq

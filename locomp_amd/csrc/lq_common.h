@@ -64,6 +64,42 @@ __device__ __forceinline__ void store_f32(void* p, size_t i, float v) {
   else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
 }
 
+// Scale / output dtype given at run time (the kernel's sd / od arguments):
+// the instantiations for bf16 and fp32 activations use it to bound their
+// number.
+constexpr int kRT = -1;
+template <int SD>
+__device__ __forceinline__ int scale_size(int sd_rt) {
+  const int sd = SD == kRT ? sd_rt : SD;
+  return sd == LQ_F32 ? 4 : 2;
+}
+template <int SD>
+__device__ __forceinline__ float load_scale(const uint8_t* p, int sd_rt) {
+  const int sd = SD == kRT ? sd_rt : SD;
+  if (sd == LQ_F32) return *reinterpret_cast<const float*>(p);
+  if (sd == LQ_F16) return float(*reinterpret_cast<const half_t*>(p));
+  return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+}
+template <int OD>
+__device__ __forceinline__ void store_out(void* O, size_t i, float v, int od_rt) {
+  if constexpr (OD != kRT) {
+    store_f32<OD>(O, i, v);
+  } else {
+    if (od_rt == LQ_F32) store_f32<LQ_F32>(O, i, v);
+    else if (od_rt == LQ_F16) store_f32<LQ_F16>(O, i, v);
+    else store_f32<LQ_BF16>(O, i, v);
+  }
+}
+
+// Element i of a scale array of dtype SD (kRT: sd_rt), as fp32.
+template <int SD>
+__device__ __forceinline__ float load_f32_rt(const void* p, size_t i, int sd_rt) {
+  const int sd = SD == kRT ? sd_rt : SD;
+  if (sd == LQ_F32) return static_cast<const float*>(p)[i];
+  if (sd == LQ_F16) return float(static_cast<const half_t*>(p)[i]);
+  return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
 // ------------------------------------------------------ bit-level unpack --
 
 __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
@@ -140,6 +176,16 @@ __device__ __forceinline__ u32x4_t int4x8_biased_kperm(uint32_t w) {
   r.y = and_or(w >> 4, 0x000F000Fu, magic);    // (k1, k5)
   r.z = and_or(w >> 8, 0x000F000Fu, magic);    // (k2, k6)
   r.w = and_or(w >> 12, 0x000F000Fu, magic);   // (k3, k7)
+  return r;
+}
+
+// The same with the OR mask as an argument (0x43004300 gives bf16 128 + q).
+__device__ __forceinline__ u32x4_t int4x8_biased_kperm_m(uint32_t w, uint32_t magic) {
+  u32x4_t r;
+  r.x = and_or(w, 0x000F000Fu, magic);
+  r.y = and_or(w >> 4, 0x000F000Fu, magic);
+  r.z = and_or(w >> 8, 0x000F000Fu, magic);
+  r.w = and_or(w >> 12, 0x000F000Fu, magic);
   return r;
 }
 

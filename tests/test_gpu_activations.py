@@ -1,0 +1,167 @@
+"""GPU parity for bf16 and fp32 activations (the reference's own kernels take
+fp32 `locomp.Tensor` activations, examples/38_quantized_matmul.py:30-40, and
+its frontend types bf16 parameters as locomp.BFloat16, locomp/frontend.py:53).
+
+Both run on bf16 MFMAs with exact integer weights and fp32 group scales:
+bf16 activations as given, fp32 ones split exactly into three bf16 parts.
+The oracle is the restated reference NumPy path on the same values (bf16
+activations widened exactly to fp32).  Bars: rtol / atol 1e-2 for bf16
+activations; rtol 1e-4 (+ atol 1e-5 max|Y|) for fp32.
+"""
+
+import numpy as np
+import pytest
+
+from locomp_amd import synth
+from oracle import quant_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+lq = pytest.importorskip("locomp_amd")
+
+
+def _bf16_round(a):
+    return ref.bf16_bits_to_f32(ref.f32_to_bf16_bits(np.asarray(a, np.float32))).reshape(np.shape(a))
+
+
+def _dev(a, name):
+    if name == "bf16":
+        return lq.tensor(np.asarray(a, np.float32), dtype=lq.bfloat16)
+    return lq.tensor(np.ascontiguousarray(a.astype({"f32": np.float32, "f16": np.float16}[name])))
+
+
+def _run(wbits, X, W, S, N, K, G, xd, sd, od):
+    M = X.shape[0]
+    Og = lq.empty((M, N), lq.bfloat16 if od == "bf16" else {"f32": np.float32, "f16": np.float16}[od])
+    Xg, Sg = _dev(X, xd), _dev(S, sd)
+    if wbits == 4:
+        lq.dequant_matvec_int4[(N,), (128,)](Xg, lq.tensor(W), Sg, Og, K, K // 2, K // G, G)
+    else:
+        lq.dequant_matvec_int8[(N,), (128,)](Xg, lq.tensor(W), Sg, Og, K, K // G, G)
+    got = Og.numpy()
+    if od == "bf16":
+        return ref.bf16_bits_to_f32(got).reshape(M, N)
+    return got.astype(np.float32)
+
+
+def _used(a, name):
+    """The values the kernel sees for an array uploaded as `name`."""
+    if name == "bf16":
+        return _bf16_round(a)
+    if name == "f16":
+        return np.asarray(a).astype(np.float16).astype(np.float32)
+    return np.asarray(a, np.float32)
+
+
+def _oracle(wbits, X, W, S, G):
+    f = ref.fast_numpy_matvec_int4 if wbits == 4 else ref.fast_numpy_matvec_int8
+    return f(X, W, S, G)
+
+
+def _case(wbits, M, N, K, G, seed, lo=0.001, hi=0.01):
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, lo, hi, x_dtype=np.float32,
+                                s_dtype=np.float32, seed=seed)
+    return X, W, S
+
+
+# ------------------------------------------------------------- bf16 X --
+
+@pytest.mark.parametrize("wbits", [4, 8])
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_bf16_activations_cfg3(wbits, M):
+    """BASELINE cfg 3 shape (11008 x 4096, G = 128) with bf16 activations and
+    bf16 outputs, full output against the oracle."""
+    N, K, G = 11008, 4096, 128
+    X, W, S = _case(wbits, M, N, K, G, seed=M + wbits)
+    got = _run(wbits, X, W, S, N, K, G, "bf16", "f16", "bf16")
+    want = _oracle(wbits, _used(X, "bf16"), W, _used(S, "f16"), G)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("wbits,M,N,K,G", [
+    (4, 2, 300, 2048, 32),       # two / four scale groups per wave eighth
+    (4, 5, 257, 4096, 64),
+    (4, 3, 640, 11008, 128),     # partial last 512-byte chunk
+    (4, 16, 96, 1024, 1024),
+    (8, 1, 1000, 4096, 4096),    # per-channel
+    (8, 7, 333, 2064, 16),       # partial chunk, 16-k groups
+    (8, 16, 130, 11008, 128),
+    (8, 2, 64, 1536, 64),
+])
+@pytest.mark.parametrize("sd,od", [("f16", "f16"), ("bf16", "bf16"), ("f32", "f32"), ("f16", "bf16")])
+def test_bf16_activations_shapes(wbits, M, N, K, G, sd, od):
+    X, W, S = _case(wbits, M, N, K, G, seed=M * 7 + N + K)
+    got = _run(wbits, X, W, S, N, K, G, "bf16", sd, od)
+    want = _oracle(wbits, _used(X, "bf16"), W, _used(S, sd), G)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("wbits,M,N,K,G", [
+    (4, 2048, 4096, 4096, 128),   # BASELINE cfg 5a with bf16 activations
+    (4, 128, 4096, 4096, 128),    # split-K (8 ways)
+    (8, 512, 4096, 4096, 128),
+    (4, 96, 200, 1024, 64),
+    (8, 300, 257, 2048, 2048),
+])
+def test_bf16_activations_prefill(wbits, M, N, K, G):
+    """bf16 prefill on the MFMA GEMM (bf16 MFMAs on exact integer weights,
+    fp32 group scales), every output row against the oracle."""
+    X, W, S = _case(wbits, M, N, K, G, seed=M + N + wbits)
+    got = _run(wbits, X, W, S, N, K, G, "bf16", "f16", "bf16")
+    want = _oracle(wbits, _used(X, "bf16"), W, _used(S, "f16"), G)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+
+
+# ------------------------------------------------------------- fp32 X --
+
+def _close32(got, want):
+    atol = 1e-5 * max(1.0, float(np.abs(want).max()))
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=atol)
+
+
+def test_fp32_activations_cfg1():
+    """BASELINE cfg 1 (the reference's CPU config): W8A32, X fp32 [4, 512],
+    int8 [512, 512], per-output-channel fp32 scales, fp32 output."""
+    rng = np.random.default_rng(0)
+    X = rng.standard_normal((4, 512)).astype(np.float32)
+    W = rng.integers(-127, 128, (512, 512)).astype(np.int8)
+    S = rng.uniform(0.005, 0.02, (512, 1)).astype(np.float32)
+    got = _run(8, X, W, S, 512, 512, 512, "f32", "f32", "f32")
+    _close32(got, ref.fast_numpy_matvec_int8(X, W, S, 512))
+
+
+@pytest.mark.parametrize("wbits", [4, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_fp32_activations_cfg3(wbits, M):
+    """cfg 3 shape with fp32 activations / scales / outputs (the reference's
+    dtypes), full output, rtol 1e-4."""
+    N, K, G = 11008, 4096, 128
+    X, W, S = _case(wbits, M, N, K, G, seed=10 + M + wbits)
+    got = _run(wbits, X, W, S, N, K, G, "f32", "f32", "f32")
+    _close32(got, _oracle(wbits, X, W, S, G))
+
+
+@pytest.mark.parametrize("wbits,M,N,K,G,sd", [
+    (4, 1, 333, 2048, 32, "f16"), (4, 4, 100, 11008, 128, "f32"), (4, 3, 640, 4096, 64, "bf16"),
+    (8, 2, 257, 2064, 16, "f32"), (8, 4, 96, 4096, 4096, "f16"), (8, 1, 1000, 1024, 128, "f32")])
+def test_fp32_activations_shapes(wbits, M, N, K, G, sd):
+    X, W, S = _case(wbits, M, N, K, G, seed=M + N + K)
+    X = X * np.float32(3.0)   # values across several binades
+    got = _run(wbits, X, W, S, N, K, G, "f32", sd, "f32")
+    _close32(got, _oracle(wbits, X, W, _used(S, sd), G))
+
+
+def test_fp32_split_is_exact_on_hard_values():
+    """Activations with 24 significant bits, tiny and huge magnitudes: the
+    three-part split must reproduce fp32 products (one weight row of ones,
+    so Y = scale * sum(x) is known in float64)."""
+    rng = np.random.default_rng(5)
+    K, N, G = 2048, 32, 2048
+    X = (rng.standard_normal((1, K)) * np.exp2(rng.integers(-20, 20, (1, K)))).astype(np.float32)
+    W = np.full((N, K), 1, np.int8)
+    S = np.ones((N, 1), np.float32)
+    got = _run(8, X, W, S, N, K, G, "f32", "f32", "f32")
+    want = np.full((1, N), X.astype(np.float64).sum(), np.float64)
+    scale = np.abs(X.astype(np.float64)).sum()
+    # one bf16 part would err by ~2^-9 of the largest terms (~1e-3 of scale)
+    assert np.abs(got - want).max() <= 2e-5 * scale
