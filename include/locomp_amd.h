@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define LOCOMP_AMD_ABI_VERSION 4
+#define LOCOMP_AMD_ABI_VERSION 5
 
 /* Element dtype codes. */
 enum {
@@ -60,7 +60,8 @@ enum {
   LQ_ERR_DTYPE = -2,   /* unknown dtype code                          */
   LQ_ERR_NULL = -3,    /* null pointer with a non-empty problem        */
   LQ_ERR_POLICY = -4,  /* unknown kernel policy                        */
-  LQ_ERR_SCRATCH = -5  /* needs more scratch than the fixed buffer holds */
+  LQ_ERR_SCRATCH = -5, /* needs more scratch than the fixed buffer holds */
+  LQ_ERR_NAME = -6     /* unknown kernel name (locomp_amd_launch)        */
 };
 
 /* Quantizer variants (locomp_amd_quantize_int4). */
@@ -174,6 +175,32 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
                                             int64_t NUM_SCALES, int64_t GROUP_SIZE, int64_t I,
                                             int64_t M, int x_dtype, int scale_dtype, int out_dtype,
                                             void* stream);
+
+/* One entry for every kernel above, in the reference's generated-launcher
+ * convention: locomp_launch_<name>(grid_x, grid_y, block_x, block_y,
+ * void** args) (locomp/backends/rocm_codegen.py:304-340, called from
+ * locomp/api.py:985-990) takes args[i] = the device pointer of the i-th
+ * pointer parameter in signature order and bakes the integer parameters into
+ * the generated code; here the kernel is chosen by `name` and the integer
+ * parameters are passed as values, in signature order:
+ *   "dequant_int4"         (W, SCALES, OUT; K, HALF_K, NUM_SCALES, GROUP_SIZE)
+ *                          examples/52_dequantize.py:27-53
+ *   "dequant_int8"         (W, SCALES, OUT; K, NUM_SCALES, GROUP_SIZE)
+ *                          examples/52_dequantize.py:60-74
+ *   "dequant_matvec_int4"  (X, W, scales, O; K_dim, HALF_K, NUM_SCALES, GROUP_SIZE)
+ *                          examples/38_quantized_matmul.py:30-87
+ *   "dequant_matvec_int8", "quant_matvec_int8"
+ *                          (X, W, scales, O; K_dim, NUM_SCALES, GROUP_SIZE)
+ *                          examples/38_quantized_matmul.py:94-134,
+ *                          examples/58_benchmark_suite.py:241-264
+ * grid_x = N (the reference's grid (N,)); grid_y must be 1 and the block at
+ * most 1024 threads (the kernels pick their own geometry).  dtypes[i] = the
+ * element dtype code of pointer parameter i (ignored for the weights); m =
+ * activation rows of X (1 for the reference's matvec).  Returns what the
+ * matching entry point returns, LQ_ERR_NAME for an unknown name. */
+int locomp_amd_launch(const char* name, int grid_x, int grid_y, int block_x, int block_y,
+                      void** args, const int64_t* constexprs, int n_constexprs,
+                      const int* dtypes, int64_t m, void* stream);
 
 /* Quantize float weights W [N, K] (in_dtype fp32 / fp16 / bf16) on the GPU
  * into PACKED uint8 [N, K/2] (byte j = q[2j] | q[2j+1] << 4) and float32

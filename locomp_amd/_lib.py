@@ -13,12 +13,12 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_liblocomp_amd.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # dtype codes (LQ_F32 / LQ_F16 / LQ_BF16)
 F32, F16, BF16 = 0, 1, 2
 # error codes
-OK, ERR_SHAPE, ERR_DTYPE, ERR_NULL, ERR_POLICY, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
+OK, ERR_SHAPE, ERR_DTYPE, ERR_NULL, ERR_POLICY, ERR_SCRATCH, ERR_NAME = 0, -1, -2, -3, -4, -5, -6
 # kernel policies
 POLICY_AUTO, POLICY_GENERIC = 0, 1
 # quantizer variants (LQ_QUANT_EX38 / LQ_QUANT_EX52)
@@ -44,6 +44,8 @@ SIGNATURES = {
                                        _int, _int, _int, _vp],
     "locomp_amd_dequant_matvec_int4_silu_mul": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                                 _i64, _int, _int, _int, _vp],
+    "locomp_amd_launch": [ctypes.c_char_p, _int, _int, _int, _int, ctypes.POINTER(_vp),
+                          ctypes.POINTER(_i64), _int, ctypes.POINTER(_int), _i64, _vp],
     "locomp_amd_quantize_int4": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp],
     "locomp_amd_quantize_int8": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
     "locomp_amd_stream_read": [_vp, _i64, _vp, _vp],

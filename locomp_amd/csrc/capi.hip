@@ -1,6 +1,7 @@
 // C ABI entry points: argument validation and kernel selection.
 // Declarations and conventions: include/locomp_amd.h.
 #include <atomic>
+#include <string>
 
 #include "lq_common.h"
 
@@ -120,6 +121,7 @@ const char* locomp_amd_strerror(int code) {
     case LQ_ERR_NULL: return "null pointer for a non-empty problem";
     case LQ_ERR_POLICY: return "unknown kernel policy";
     case LQ_ERR_SCRATCH: return "problem needs more scratch than the fixed buffer holds";
+    case LQ_ERR_NAME: return "unknown kernel name";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -244,6 +246,47 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
   }
   return launch_generic_silu(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
                              out_dtype, st);
+}
+
+// The reference's generated-launcher convention (args = device pointers of
+// the pointer parameters in signature order), with the integer parameters
+// the reference bakes into each generated launcher passed as values.
+int locomp_amd_launch(const char* name, int grid_x, int grid_y, int block_x, int block_y,
+                      void** args, const int64_t* constexprs, int n_constexprs,
+                      const int* dtypes, int64_t m, void* stream) {
+  if (name == nullptr) return LQ_ERR_NAME;
+  if (grid_x < 0 || grid_y != 1 || block_x <= 0 || block_y <= 0 ||
+      int64_t(block_x) * block_y > 1024)
+    return LQ_ERR_SHAPE;
+  const std::string n(name);
+  const int64_t N = grid_x;
+  // every kernel here has pointer arguments and integer parameters
+  auto need = [&](int nc) {
+    return args != nullptr && dtypes != nullptr && constexprs != nullptr && n_constexprs == nc;
+  };
+  if (n == "dequant_int4") {        // (W, SCALES, OUT; K, HALF_K, NUM_SCALES, GROUP_SIZE)
+    if (!need(4)) return LQ_ERR_SHAPE;
+    return locomp_amd_dequant_int4(args[0], args[1], args[2], constexprs[0], constexprs[1],
+                                   constexprs[2], constexprs[3], N, dtypes[1], dtypes[2], stream);
+  }
+  if (n == "dequant_int8") {        // (W, SCALES, OUT; K, NUM_SCALES, GROUP_SIZE)
+    if (!need(3)) return LQ_ERR_SHAPE;
+    return locomp_amd_dequant_int8(args[0], args[1], args[2], constexprs[0], constexprs[1],
+                                   constexprs[2], N, dtypes[1], dtypes[2], stream);
+  }
+  if (n == "dequant_matvec_int4") { // (X, W, scales, O; K_dim, HALF_K, NUM_SCALES, GROUP_SIZE)
+    if (!need(4)) return LQ_ERR_SHAPE;
+    return locomp_amd_dequant_matvec_int4(args[0], args[1], args[2], args[3], constexprs[0],
+                                          constexprs[1], constexprs[2], constexprs[3], N, m,
+                                          dtypes[0], dtypes[2], dtypes[3], stream);
+  }
+  if (n == "dequant_matvec_int8" || n == "quant_matvec_int8") {   // (X, W, scales, O; K_dim, NUM_SCALES, GROUP_SIZE)
+    if (!need(3)) return LQ_ERR_SHAPE;
+    return locomp_amd_dequant_matvec_int8(args[0], args[1], args[2], args[3], constexprs[0],
+                                          constexprs[1], constexprs[2], N, m, dtypes[0],
+                                          dtypes[2], dtypes[3], stream);
+  }
+  return LQ_ERR_NAME;
 }
 
 // Quantizers.  mode: 0 = examples/38 quantize_int4, 1 = examples/52
