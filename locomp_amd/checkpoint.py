@@ -69,8 +69,13 @@ def _to_device(t):
     return tensor(t.to(torch.float32).contiguous().numpy())
 
 
-def quantize_checkpoint(path, group_size=32, scale_dtype=np.float16, select=None):
-    """Quantize the selected 2-D weights of a safetensors file on the GPU."""
+def quantize_checkpoint(path, group_size=32, scale_dtype=np.float32, select=None):
+    """Quantize the selected 2-D weights of a safetensors file on the GPU.
+
+    Scales stay float32 by default, as the reference's producers return them
+    (examples/52_dequantize.py:126); ``scale_dtype=np.float16`` halves their
+    size and raises ``ValueError`` if a scale overflows to inf or a nonzero
+    one underflows to zero in fp16."""
     from safetensors import safe_open
 
     from .quantize import quantize_int4
@@ -89,7 +94,13 @@ def quantize_checkpoint(path, group_size=32, scale_dtype=np.float16, select=None
             P, S = quantize_int4(dev, group_size, as_tensors=True)
             dev.free()
             if np.dtype(scale_dtype) == np.float16:      # cast on the device
-                S = Tensor(S.torch.to(_torch().float16), np.dtype(np.float16), S.shape)
+                s32 = S.torch
+                s16 = s32.to(_torch().float16)
+                bad = _torch().isinf(s16) | ((s16 == 0) & (s32 != 0))
+                if bool(bad.any()):
+                    raise ValueError(f"{name}: {int(bad.sum())} scales do not fit float16 "
+                                     "(overflow or underflow); use scale_dtype=np.float32")
+                S = Tensor(s16, np.dtype(np.float16), S.shape)
             elif np.dtype(scale_dtype) != np.float32:
                 raise ValueError("scale_dtype must be float16 or float32")
             out[name] = QuantizedLinear(P, S, shape[0], shape[1], group_size)

@@ -224,14 +224,17 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
   if (K_dim == 0) return launch_zero_fill(O, M * I, out_dtype, st);   // silu(0) * 0
   if (!X || !W || !scales) return LQ_ERR_NULL;
   const int64_t N = 2 * I;
-  const bool fast = fast_allowed() && x_dtype == LQ_F16 && aligned(X, 16) && aligned(W, 16) &&
-                    aligned(scales, 4) &&
-                    M * K_dim <= kMax32 && N * HALF_K <= kMax32 && N * NUM_SCALES <= kMax32 &&
-                    scale_dtype != LQ_BF16 && out_dtype != LQ_BF16;
+  const bool fast = fast_allowed() && aligned(X, 16) && aligned(W, 16) && aligned(scales, 4) &&
+                    M * K_dim <= kMax32 && N * HALF_K <= kMax32 && N * NUM_SCALES <= kMax32;
+  // the fused epilogues are instantiated for fp16 activations with fp16 /
+  // fp32 scales and outputs; bf16 ones and bf16 / fp32 activations take the
+  // staged path below (fast matvec, then the pairwise epilogue)
+  const bool fused = x_dtype == LQ_F16 && scale_dtype != LQ_BF16 && out_dtype != LQ_BF16;
   if (fast) {
-    if (M > 64 && K_dim % 64 == 0)   // prefill: the MFMA GEMM with the epilogue
+    rc = LQ_ERR_SHAPE;
+    if (fused && M > 64 && K_dim % 64 == 0)   // prefill: the MFMA GEMM with the epilogue
       rc = launch_gemm_silu(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
-    else
+    else if (fused)
       rc = launch_silu_fast(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
     if (rc != LQ_ERR_SHAPE) return rc;
     // No fused kernel for this shape: the fast matvec into an fp32 staging

@@ -40,7 +40,7 @@ def test_quantize_checkpoint_matches_reference_producer(tmp_path):
 def test_packed_file_round_trip_and_matvec(tmp_path):
     src = tmp_path / "model.safetensors"
     w = _write_checkpoint(src)
-    layers = lq.quantize_checkpoint(src, group_size=32)          # fp16 scales
+    layers = lq.quantize_checkpoint(src, group_size=32, scale_dtype=np.float16)
     dst = tmp_path / "model.int4.safetensors"
     lq.save_packed(dst, layers)
     back = lq.load_packed(dst)
@@ -53,3 +53,20 @@ def test_packed_file_round_trip_and_matvec(tmp_path):
         y = layer(x).astype(np.float32)
         want = ref.fast_numpy_matvec_int4(x, p, s.astype(np.float16), 32)
         np.testing.assert_allclose(y, want, rtol=1e-2, atol=1e-2 * max(1.0, float(np.abs(want).max()) / 100))
+
+
+def test_default_scales_are_float32_and_fp16_overflow_is_an_error(tmp_path):
+    import torch
+    from safetensors.torch import save_file
+    src = tmp_path / "m.safetensors"
+    w = torch.zeros(64, 64)
+    w[0, :32] = 1e6          # group amax 1e6 -> scale 1.4e5: beyond fp16
+    w[1, :32] = 1e-12        # scale 1.4e-13: zero in fp16
+    w[2:] = torch.randn(62, 64)
+    save_file({"l.weight": w}, str(src))
+    layers = lq.quantize_checkpoint(src, group_size=32)
+    p, s = ref.quantize_int4(w.numpy(), 32)
+    assert layers["l.weight"].scales.numpy().dtype == np.float32
+    assert np.array_equal(layers["l.weight"].scales.numpy().view(np.uint32), s.view(np.uint32))
+    with pytest.raises(ValueError, match="float16"):
+        lq.quantize_checkpoint(src, group_size=32, scale_dtype=np.float16)

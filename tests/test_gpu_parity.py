@@ -79,6 +79,40 @@ def test_dequant_int8_bitexact(policy, sd, od, N, K, G):
     assert np.array_equal(_bits(got), _bits(want))
 
 
+@pytest.mark.parametrize("wbits", [4, 8])
+@pytest.mark.parametrize("sd", ["f16", "f32"])
+@pytest.mark.parametrize("od", ["f16", "f32", "bf16"])
+def test_dequant_bitexact_subnormal_and_negative_scales(wbits, sd, od):
+    """Scales whose products are fp16 subnormals (|s| down to 2^-24, so
+    (q - 8) s lands below 2^-14), zero, negative (q = 8 then gives -0.0),
+    and large ones near the fp16 limit; every output bit must match the
+    reference definition, through the fast kernels and the generic ones."""
+    N, K, G = 48, 256, 32
+    rng = np.random.default_rng(wbits * 10 + len(sd) + len(od))
+    W, _ = synth.dequant_case(wbits, N, K, G, 0.001, 0.01, seed=3)
+    mags = np.concatenate([np.exp2(rng.uniform(-24, -14, 180)),      # subnormal products
+                           np.exp2(rng.uniform(-14, 4, 180)),
+                           [0.0] * 8, [2.0 ** -24] * 8, [6.0e4 / 2048] * 8])   # N * K / G = 384
+    sign = np.where(rng.random(mags.size) < 0.5, -1.0, 1.0)
+    S = (mags * sign).reshape(N, K // G).astype(NP_OF[sd])
+    for pol in (0, 1):
+        lq.set_policy(pol)
+        try:
+            if wbits == 4:
+                got = _run_dequant4(W, S, N, K, G, od)
+                want = ref.cast_out(ref.dequant_int4_ref(W, S, N, K, G), od)
+            else:
+                got = _run_dequant8(W, S, N, K, G, od)
+                want = ref.cast_out(ref.dequant_int8_ref(W, S, N, K, G), od)
+        finally:
+            lq.set_policy(0)
+        assert np.array_equal(_bits(got), _bits(want)), f"policy {pol}"
+        if od == "f16" and sd == "f16":
+            w16 = np.ascontiguousarray(want).view(np.uint16)
+            assert ((w16 & 0x7C00) == 0).any() and ((w16 & 0x7FFF) != 0).any()   # subnormals present
+            assert (w16 == 0x8000).any() or wbits == 8                          # -0.0 from q = 8
+
+
 def test_dequant_int4_cfg2_full_bitexact():
     c = synth.CFG2
     W, S = synth.dequant_case(4, c["N"], c["K"], c["G"], c["lo"], c["hi"])
@@ -185,9 +219,7 @@ def test_int8_prefill_large():
     M, N, K, G = 512, 4096, 4096, 128
     X, W, S = synth.matvec_case(8, M, N, K, G, 0.002, 0.02, seed=8)
     got = _matvec(8, X, W, S, N, K, G, "f16")
-    rows = np.r_[0:32, 250:282, M - 32:M]
-    _close(got[rows], _oracle(8, X[rows], W, S, G))
-    assert np.isfinite(got.astype(np.float32)).all()
+    _close(got, _oracle(8, X, W, S, G))
 
 
 # Decode (M <= 4) with K not a multiple of 2048: the 2048-k segment kernel
@@ -225,6 +257,35 @@ def test_matvec_tile_partial_chunk(wbits, M, N, K, G):
     _close(got, _oracle(wbits, X, W, S, G))
 
 
+@pytest.mark.parametrize("wbits,G", [(4, 32), (4, 64), (8, 16), (8, 64), (8, 128)])
+@pytest.mark.parametrize("sd,od", [("bf16", "f16"), ("f16", "bf16"), ("bf16", "bf16"), ("bf16", "f32")])
+@pytest.mark.parametrize("M,N", [(1, 1001), (4, 333), (16, 130), (40, 257)])
+def test_matvec_bf16_scales_or_output_groups(wbits, G, sd, od, M, N):
+    """bf16 scales / outputs with int4 and int8 weights, the tile kernels'
+    multi-group scale reads (2 or 4 groups per wave eighth), the (bf16
+    scales, fp32 output) pair, and ragged N whose scale array is not a whole
+    number of dwords for odd N (those shapes take the kernels that read
+    scales per element)."""
+    K = 2048
+    X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=M + N + G + wbits)
+    S = S.astype(np.float32)
+    if sd == "bf16":
+        S_used = ref.bf16_bits_to_f32(ref.f32_to_bf16_bits(S)).reshape(S.shape)
+        Sg = _up(S, "bf16")
+    else:
+        S_used = S.astype(np.float16).astype(np.float32)
+        Sg = _up(S.astype(np.float16))
+    Og = lq.empty((M, N), _dtype(od))
+    if wbits == 4:
+        lq.dequant_matvec_int4[(N,), (128,)](_up(X), _up(W), Sg, Og, K, K // 2, K // G, G)
+    else:
+        lq.dequant_matvec_int8[(N,), (128,)](_up(X), _up(W), Sg, Og, K, K // G, G)
+    got = Og.numpy()
+    got = ref.bf16_bits_to_f32(got).reshape(M, N) if od == "bf16" else got.astype(np.float32)
+    want = _oracle(wbits, X, W, S_used, G)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+
+
 @pytest.mark.parametrize("sd,od", [("bf16", "f16"), ("f16", "bf16"), ("bf16", "bf16"), ("f32", "bf16")])
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 4096), (1, 300, 6144), (3, 200, 2048), (4, 1000, 4096),
                                    (16, 300, 2048), (1, 200, 11008), (40, 300, 2048)])
@@ -250,8 +311,8 @@ def test_matvec_int4_bf16_scales_or_output(sd, od, M, N, K):
     got = Og.numpy()
     got = ref.bf16_bits_to_f32(got).reshape(M, N) if od == "bf16" else got.astype(np.float32)
     want = ref.fast_numpy_matvec_int4(X, W, S_used, G)
-    tol = 1e-2 if od != "bf16" else 2e-2   # bf16 output: 8-bit mantissa (rel 2^-9)
-    np.testing.assert_allclose(got, want, rtol=tol, atol=1e-2)
+    # the 1e-2 bar holds for bf16 outputs too (their rounding adds 2^-9 relative)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
 
 
 # Split-K prefill (fewer 128 x 128 output tiles than CUs): k split 8, 6, 4
@@ -276,25 +337,21 @@ def test_matmul_prefill_split_k(wbits, M, N, K, G, od):
 
 def test_int8_prefill_forced_split_big_tiles():
     """256-row tiles with more int8 scale groups (65) than LDS stages: K is
-    split in two although the tiles fill the CUs (oracle on a row subset)."""
+    split in two although the tiles fill the CUs (every output checked)."""
     M, N, K, G = 2048, 4096, 8320, 128
     X, W, S = synth.matvec_case(8, M, N, K, G, 0.002, 0.02, seed=12)
     got = _matvec(8, X, W, S, N, K, G, "f16")
-    rows = np.r_[0:32, 1000:1032, M - 32:M]
-    _close(got[rows], _oracle(8, X[rows], W, S, G))
-    assert np.isfinite(got.astype(np.float32)).all()
+    _close(got, _oracle(8, X, W, S, G))
 
 
 @pytest.mark.parametrize("wbits", [4, 8])
 def test_prefill_big_tiles_split_two(wbits):
     """128 <= 256-row tiles < 256 CUs: 256 x 128 tiles with k split in two
-    (oracle on a row subset)."""
+    (every output checked)."""
     M, N, K, G = 1024, 4096, 2048, 128
     X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=21 + wbits)
     got = _matvec(wbits, X, W, S, N, K, G, "f16")
-    rows = np.r_[0:40, 500:540, M - 40:M]
-    _close(got[rows], _oracle(wbits, X[rows], W, S, G))
-    assert np.isfinite(got.astype(np.float32)).all()
+    _close(got, _oracle(wbits, X, W, S, G))
 
 
 def test_matmul_prefill_split_k_graph():
@@ -351,10 +408,7 @@ def test_cfg5a_prefill_full():
     c = synth.CFG5A
     X, W, S = synth.matvec_case(4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"])
     got = _matvec(4, X, W, S, c["N"], c["K"], c["G"], "f16")
-    # Oracle on a row subset (the full fp32 product is 69 GFLOP on the host).
-    rows = np.r_[0:64, 1000:1064, c["M"] - 64:c["M"]]
-    _close(got[rows], _oracle(4, X[rows], W, S, c["G"]))
-    assert np.isfinite(got.astype(np.float32)).all()
+    _close(got, _oracle(4, X, W, S, c["G"]))     # every output (BLAS on the host)
 
 
 def test_reference_fp32_matvec_api():
@@ -444,5 +498,32 @@ def test_matvec_int4_silu_mul(policy, M, I, K, G, xd):
     S = lq.interleave_gate_up(Sg, Su)
     got = lq.gpu_matvec_int4_silu_mul(Xa, W, S, G).astype(np.float64)
     want, bound = _silu_mul_oracle(Xa, Wg, Sg, Wu, Su, G)
+    err = np.abs(got - want)
+    assert (err <= bound).all(), (err.max(), np.argmax(err - bound))
+
+
+@pytest.mark.parametrize("M,I,K,G", [(1, 1536, 576, 32), (4, 700, 2048, 128), (40, 300, 2048, 64),
+                                     (130, 256, 1024, 128)])
+@pytest.mark.parametrize("xd,sd,od", [("f16", "bf16", "bf16"), ("bf16", "f16", "bf16"),
+                                      ("bf16", "bf16", "f32"), ("f32", "f32", "f32")])
+def test_matvec_int4_silu_mul_other_dtypes(M, I, K, G, xd, sd, od):
+    """bf16 scales / outputs and bf16 / fp32 activations: the fast matvec
+    into the staged fp32 buffer, then the pairwise epilogue."""
+    Xa, Wg, Sg = synth.matvec_case(4, M, I, K, G, 0.01, 0.05, x_dtype=np.float32,
+                                   s_dtype=np.float32, seed=I + K + 7)
+    _, Wu, Su = synth.matvec_case(4, M, I, K, G, 0.01, 0.05, x_dtype=np.float32,
+                                  s_dtype=np.float32, seed=I + K + 8)
+    used = {"bf16": lambda a: ref.bf16_bits_to_f32(ref.f32_to_bf16_bits(a)).reshape(a.shape),
+            "f16": lambda a: a.astype(np.float16).astype(np.float32), "f32": lambda a: a}
+    Xu, Sgu, Suu = used[xd](Xa), used[sd](Sg), used[sd](Su)
+    W = lq.interleave_gate_up(Wg, Wu)
+    S = lq.interleave_gate_up(Sg, Su)
+    Xg = _up(Xa, "bf16") if xd == "bf16" else _up(Xa.astype(_dtype(xd)))
+    Sdev = _up(S, "bf16") if sd == "bf16" else _up(S.astype(_dtype(sd)))
+    got = lq.gpu_matvec_int4_silu_mul(Xg, W, Sdev, G, out_dtype=_dtype(od))
+    got = (ref.bf16_bits_to_f32(got).reshape(M, I) if od == "bf16" else got).astype(np.float64)
+    want, bound = _silu_mul_oracle(Xu, Wg, Sgu, Wu, Suu, G)
+    if od == "bf16":
+        bound = bound + 2.0 ** -8 * np.abs(want)
     err = np.abs(got - want)
     assert (err <= bound).all(), (err.max(), np.argmax(err - bound))

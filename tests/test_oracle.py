@@ -178,6 +178,41 @@ def test_quantize_round_trip_and_ties():
     assert s[0, 0] == 1.0 and (p == 0x88).all()
 
 
+def test_quantize_int8_ties_to_even():
+    """quantize_int8 (examples/38_quantized_matmul.py:274-291): amax = 127
+    makes the scale exactly 1.0, so x.5 values are exact ties; np.round sends
+    them to the even integer (half-away-from-zero would give 1, 3, 3, -1, -2,
+    127)."""
+    g = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, 126.5, 0.0] * 4], np.float32)
+    q, s = ref.quantize_int8(g, 32)
+    assert s[0, 0] == np.float32(1.0)
+    assert list(q[0, :8]) == [127, 0, 2, 2, 0, -2, 126, 0]
+    q, s = ref.quantize_int8(np.zeros((1, 32), np.float32), 32)     # amax 0 -> scale 1
+    assert s[0, 0] == 1.0 and (q == 0).all()
+
+
+def test_quantize_int4_ref_ties_floor_and_bias():
+    """quantize_int4_ref (examples/52_dequantize.py:110-126): scale =
+    max(amax, 1e-10) / 7 and q = round(w / (scale + 1e-10)) + 8."""
+    # ties: amax 7 -> scale 1.0; 1.0 + 1e-10 rounds to 1.0 in float32
+    g = np.array([[7.0, 0.5, 1.5, 2.5, -0.5, -1.5, 3.5, 0.0] * 4], np.float32)
+    p, s = ref.quantize_int4_ref(g, 32)
+    assert s[0, 0] == np.float32(1.0)
+    assert list(ref.unpack_int4(p)[0][:8] + 8) == [15, 8, 10, 10, 8, 6, 12, 8]
+    # the +1e-10 in the divisor: with amax = 7 u (u = 2^-34, scale u exactly)
+    # w / (u + 1e-10) = 7 / (1 + 1e-10 / u) = 7 / 2.718 = 2.575 for w = amax:
+    # q = 8 + 3; -amax -> 8 - 3; amax / 2 -> 8 + round(1.288) = 9 (without the
+    # term: 15, 1, 12)
+    u = np.float32(2.0 ** -34)
+    g = np.array([[7 * u, -7 * u, 3.5 * u, 0.0] * 8], np.float32)
+    p, s = ref.quantize_int4_ref(g, 32)
+    assert s[0, 0] == u
+    assert list(ref.unpack_int4(p)[0][:4] + 8) == [11, 5, 9, 8]
+    # the 1e-10 floor: an all-zero group keeps a positive scale 1e-10 / 7
+    p, s = ref.quantize_int4_ref(np.zeros((1, 32), np.float32), 32)
+    assert 1.42e-11 < s[0, 0] < 1.43e-11 and (p == 0x88).all()
+
+
 def test_golden_fixtures():
     path = os.path.join(GOLDEN, "quant_golden.npz")
     g = np.load(path)  # allow_pickle=False by default
