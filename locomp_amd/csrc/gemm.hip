@@ -6,9 +6,10 @@
 // activation row (locomp examples/38_quantized_matmul.py:154).  Values follow
 // the same definition: w = (q - 8) * s[n, k / G] (int4), q * s (int8).
 //
-// Tiling (default GemmCfg<8, 1, 2, 8>: 512 lanes, BM x BN = 256 x 128, BK = 64):
-//   * Wave w owns output rows [32 w, 32 w + 32) and all 128 columns: 2 x 8
-//     tiles of v_mfma_f32_16x16x32_f16 (fp32 accumulators in VGPRs).
+// Tiling (default GemmCfg<4, 2, 4, 4>: 512 lanes, BM x BN = 256 x 128, BK = 64):
+//   * Waves form a 4 x 2 grid; each owns 64 x 64 outputs: 4 x 4 tiles of
+//     v_mfma_f32_16x16x32_f16 (fp32 accumulators in VGPRs), which reads 16 KB
+//     of LDS fragments per wave per k-step (32 x 128 waves read 20 KB).
 //   * Activations: each k-step's 256 x 64 fp16 tile is copied global -> LDS by
 //     the gfx950 direct-to-LDS load (global_load_lds_dwordx4): no VGPRs, 128 B
 //     of one row per 8 lanes, XOR-swizzled chunk order chosen through the
@@ -27,8 +28,9 @@
 //     form (build flag), which keeps the accumulators from being copied
 //     between VGPRs and AGPRs.
 //   * XCD-aware order: consecutive workgroups are dealt round-robin to the 8
-//     XCDs, so the tile sequence is arranged for each XCD to walk one 256-row
-//     block of X (2 MB at K = 4096: it stays in that XCD's 4 MB L2).
+//     XCDs, so each XCD is given a block of tiles that share activation and
+//     weight rows in its L2 (cfg 5a: 4 x 8 tiles, 1 MB of X rows and 2 MB of
+//     packed weights).
 #include <algorithm>
 #include <mutex>
 #include <type_traits>
@@ -119,11 +121,37 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 
   // XCD-aware tile order: workgroup b runs on XCD b % 8; XCD x takes the
   // contiguous slice [x * per, (x + 1) * per) of the row-major tile list.
+  // XCD-aware tile order: workgroup b runs on XCD b % 8.  When the tile grid
+  // splits into 8 equal blocks of gm x gn tiles, XCD x takes block x, with
+  // gm chosen to minimise the bytes one k-step of the block reads (gm BM
+  // activation rows + gn BN weight rows): the XCD's L2 then holds the
+  // activation rows and weight rows its tiles share (cfg 5a: 4 x 8 tiles).
+  // Otherwise XCD x takes the contiguous slice [x per, (x + 1) per) of the
+  // row-major tile list.
   const int total = tiles_m * tiles_n;
-  int t = blockIdx.x;
-  if (total % 8 == 0) t = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-  const int m0 = (t / tiles_n) * BM;
-  const int n0 = (t % tiles_n) * BN;
+  int m0, n0;
+  {
+    int t = blockIdx.x, gm = 0;
+    if (total % 8 == 0) {
+      const int per = total >> 3;
+      int best = 1 << 30;
+      for (int d = 1; d <= tiles_m && d <= per; ++d) {
+        if (tiles_m % d || per % d || tiles_n % (per / d)) continue;
+        const int cost = d * BM * 2 + (per / d) * BN * WBITS / 8;
+        if (cost < best) { best = cost; gm = d; }
+      }
+      if (gm == 0) t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    }
+    if (gm > 0) {
+      const int gn = (total >> 3) / gm, gcols = tiles_n / gn;
+      const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
+      m0 = ((xcd / gcols) * gm + local % gm) * BM;
+      n0 = ((xcd % gcols) * gn + local / gm) * BN;
+    } else {
+      m0 = (t / tiles_n) * BM;
+      n0 = (t % tiles_n) * BN;
+    }
+  }
   const int row_bytes = WBITS == 4 ? (K >> 1) : K;
   // split-K: workgroup row blockIdx.y covers k in [kbeg, kbeg + kspan) and
   // writes its fp32 partial sums to slice blockIdx.y of O
@@ -445,9 +473,9 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 }
 
 #ifndef LQ_GEMM_CFG
-#define LQ_GEMM_CFG 8, 1, 2, 8
+#define LQ_GEMM_CFG 4, 2, 4, 4
 #endif
-typedef GemmCfg<LQ_GEMM_CFG> GemmDefault;   // default: 256 x 128 tile, 8 waves of 32 x 128
+typedef GemmCfg<LQ_GEMM_CFG> GemmDefault;   // default: 256 x 128 tile, 4 x 2 waves of 64 x 64
 
 template <class C, int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O, int64_t M,
