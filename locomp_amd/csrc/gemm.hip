@@ -113,7 +113,8 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform (an SGPR): addresses derived from it stay scalar
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15;
   const int q4 = lane >> 4;
   const int wm = wave / C::WN;
@@ -165,19 +166,26 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   // holding logical chunk (L % 8) ^ (row & 7).  Eight lanes cover one row.
   constexpr int kDmaRows = BM / C::kWaves;
   constexpr int kADma = kDmaRows / 8;
+  // (buffer loads: a per-lane 32-bit byte offset fixed for the whole loop,
+  // the step's k in the scalar offset; rows past M re-read row M - 1)
   const int drow0 = wave * kDmaRows;
-  const half_t* adma_src[kADma];
+  const i32x4_t xrsrc = {int(uint32_t(reinterpret_cast<uint64_t>(X))),
+                         int(uint32_t(reinterpret_cast<uint64_t>(X) >> 32) & 0xFFFFu),
+                         int(uint32_t(M) * uint32_t(K) * 2u), 0x00020000};
+  uint32_t adma_off[kADma];
 #pragma unroll
   for (int i = 0; i < kADma; ++i) {
     const int row = drow0 + 8 * i + (lane >> 3);
     const int m = min(m0 + row, M - 1);
     const int c = (lane & 7) ^ (row & 7);
-    adma_src[i] = X + size_t(m) * K + kbeg + c * 8;
+    adma_off[i] = (uint32_t(m) * uint32_t(K) + uint32_t(kbeg + c * 8)) * 2u;
   }
+  const uint32_t as_base = lds_addr(&As[0][0]) + uint32_t(drow0 * kBK * 2);   // (scalar)
   auto dma_a = [&](int stage, int k0) {
 #pragma unroll
     for (int i = 0; i < kADma; ++i)
-      dma16(adma_src[i] + k0, &As[stage][(drow0 + 8 * i) * kBK]);
+      dma16_so(xrsrc, adma_off[i], uint32_t(k0) * 2u,
+               as_base + uint32_t(stage * BM * kBK * 2 + 8 * i * kBK * 2));
   };
 
   // B loader: Bg::kBytes weight bytes (Bg::kSpanK k) of one weight row
@@ -233,6 +241,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const half_t hs = half_t(bs);
     const half2_t s2 = {hs, hs};
     half_t* dst = Bs[stage];
+    const uint32_t magic = opaque_u32(0x64006400u);
     if constexpr (kBf) {
       // exact integers as bf16: an integer of at most 8 significant bits is
       // exact as a float, whose high half is then its bf16 pattern
@@ -279,7 +288,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #pragma unroll
       for (int i = 0; i < kBWords; ++i) {
         half2_t h[4];
-        int4x8_to_h2(bq[i], h);
+        int4x8_to_h2(bq[i], h, magic);
         u32x4_t v;
         v.x = as_u32(h[0] * s2);
         v.y = as_u32(h[1] * s2);

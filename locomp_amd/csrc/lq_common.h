@@ -113,18 +113,23 @@ __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast
 // high half 1024 + 16 * q_odd, both exact in fp16.  One packed FMA
 // h * (1, 1/16) + (-1032, -72) maps both to q - 8 exactly (the products are
 // exact and the sum is representable, so the single rounding is exact).
-__device__ __forceinline__ half2_t int4_pair_to_h2(uint32_t w, int p) {
+// `magic` = 0x64006400 (an opaque register value lets the mask and the OR
+// issue as one v_and_or_b32; with two literal constants they take two ops).
+__device__ __forceinline__ half2_t int4_pair_to_h2(uint32_t w, int p, uint32_t magic) {
   const half2_t mul = {half_t(1.0f), half_t(0.0625f)};
   const half2_t add = {half_t(-1032.0f), half_t(-72.0f)};
   const uint32_t sel = 0x00000000u | uint32_t(p) | (uint32_t(p) << 16);
   const uint32_t u = __builtin_amdgcn_perm(w, w, sel);
-  const uint32_t t = (u & 0x00F0000Fu) | 0x64006400u;
+  const uint32_t t = (u & 0x00F0000Fu) | magic;
   return __builtin_elementwise_fma(as_h2(t), mul, add);
 }
 
-__device__ __forceinline__ void int4x8_to_h2(uint32_t w, half2_t out[4]) {
+__device__ __forceinline__ void int4x8_to_h2(uint32_t w, half2_t out[4], uint32_t magic) {
 #pragma unroll
-  for (int p = 0; p < 4; ++p) out[p] = int4_pair_to_h2(w, p);
+  for (int p = 0; p < 4; ++p) out[p] = int4_pair_to_h2(w, p, magic);
+}
+__device__ __forceinline__ void int4x8_to_h2(uint32_t w, half2_t out[4]) {
+  int4x8_to_h2(w, out, 0x64006400u);
 }
 
 // Two int8 weights (bytes 2p, 2p+1 of w) -> half2 exact: (b ^ 0x80) in the
@@ -243,6 +248,15 @@ __device__ __forceinline__ void dma16(const void* g, const void* lds) {
   const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(lds));
   __asm__ volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                    :: "v"(g), "s"(a) : "memory", "m0");
+}
+// 16 bytes per lane from a raw buffer (byte offset voff + soff, soff
+// wave-uniform) to LDS (lane L -> lds + 16 L); bytes past the buffer read as 0.
+// (lds: the LDS byte address, wave-uniform)
+__device__ __forceinline__ void dma16_so(i32x4_t rsrc, uint32_t voff, uint32_t soff,
+                                         uint32_t lds) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane(lds);
+  __asm__ volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                   :: "v"(voff), "s"(rsrc), "s"(soff), "s"(a) : "memory", "m0");
 }
 __device__ __forceinline__ u32x4_t gload_b128(const void* g) {
   u32x4_t v;
