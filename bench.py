@@ -153,7 +153,14 @@ class Stack:
     (q, k, v, o, gate, up, down) at M = 1, random weights (BASELINE config 5b).
     One step = all 210 GEMVs of one token, launched back to back (in a graph)."""
 
-    def __init__(self, seed=0, G=32, fused=False, silu=False):
+    def __init__(self, seed=0, G=32, fused=False, silu=False, chain=False):
+        """chain=True (with fused and silu) feeds every launch the previous
+        one's output, in the order examples/54_smollm2_inference.py:494-554
+        runs the linears: q|k|v -> o (on the q part, standing in for the
+        attention output) -> gate|up with SiLU * mul -> down -> the next
+        layer's q|k|v.  Attention, norms and residual adds are not on the
+        quantized path and are left out."""
+        self.chain = chain and fused and silu
         """fused=True concatenates the weights of linears that read the same
         activation (q|k|v: N = 960, gate|up: N = 3072): 4 GEMVs per layer.
         silu=True (with fused) runs gate|up as the fused SiLU * mul launch
@@ -173,27 +180,30 @@ class Stack:
         if fused:
             (nq, k0), (nk, _), (nv, _), o, (ng, _), (nu, _), down = shapes
             shapes = [(nq + nk + nv, k0), o, (ng + nu, k0), down]
+        prev = self.xs[576]
         for _ in range(synth.SMOLLM2_LAYERS):
             for (N, K) in shapes:
                 W = synth.int4_weights(rng, N, K)
                 S = synth.scales(rng, N, K // G, 0.001, 0.01)
-                O = torch.empty(N, dtype=torch.float16, device="cuda")
                 epi = silu and fused and N == 2 * 1536
-                self.layers.append((N, K, G, _dev(W), _dev(S), O, epi))
-                self.algo_bytes += W.nbytes + S.nbytes + K * 2 + N * 2
+                O = torch.empty(N // 2 if epi else N, dtype=torch.float16, device="cuda")
+                x = prev if self.chain else self.xs[K]
+                self.layers.append((N, K, G, _dev(W), _dev(S), O, epi, x))
+                self.algo_bytes += W.nbytes + S.nbytes + K * 2 + (N // 2 if epi else N) * 2
+                prev = O     # (q|k|v: the o projection reads its first 576 = q)
         self.R = 1
         torch.cuda.synchronize()
 
     def launch(self, i, stream):
         vp = ctypes.c_void_p
-        for (N, K, G, W, S, O, epi) in self.layers:
+        for (N, K, G, W, S, O, epi, x) in self.layers:
             if epi:
                 rc = self.lib.locomp_amd_dequant_matvec_int4_silu_mul(
-                    vp(self.xs[K].data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
+                    vp(x.data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
                     K, K // 2, K // G, G, N // 2, 1, 1, 1, 1, stream)
             else:
                 rc = self.lib.locomp_amd_dequant_matvec_int4(
-                    vp(self.xs[K].data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
+                    vp(x.data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
                     K, K // 2, K // G, G, N, 1, 1, 1, 1, stream)
             if rc != 0:
                 raise RuntimeError(f"launch failed: {rc}")
@@ -443,6 +453,25 @@ def main():
         run_case("gemm_prefill_w4abf16_2048x4096x4096_g128",
                  Case("matvec", 4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
                       min_bytes=0, max_replicas=4, xd="bf16"), "mfma")
+    if want("launch_floor"):
+        # one 1 KB streaming read per launch: the per-launch cost of a graph
+        # node on this part, which bounds a stack of small dependent launches
+        class Tiny:
+            def __init__(self):
+                import torch
+                from locomp_amd import _lib
+                self.buf = torch.zeros(1024, dtype=torch.uint8, device="cuda")
+                self.sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+                self.lib = _lib.load()
+
+            def launch(self, i, stream):
+                vp = ctypes.c_void_p
+                if self.lib.locomp_amd_stream_read(vp(self.buf.data_ptr()), 1024,
+                                                   vp(self.sink.data_ptr()), stream) != 0:
+                    raise RuntimeError("stream_read failed")
+        per, _ = time_graph(Tiny(), 120, 5)
+        extra["launch_floor_1KB_read"] = {"us_per_launch": round(per * 1e6, 3)}
+        log("launch_floor_1KB_read", extra["launch_floor_1KB_read"])
     if want("dequant"):
         c = synth.CFG2
         run_case("dequant_int4_4096x4096_g32_f16",
@@ -450,14 +479,15 @@ def main():
     if want("quantize"):
         run_case("quantize_int4_4096x4096_g32_from_f32", QuantCase(4096, 4096, 32), "hbm")
     if want("smollm2"):
-        for fused, silu in ((False, False), (True, False), (True, True)):
-            st = Stack(fused=fused, silu=silu)
+        for fused, silu, chain in ((False, False, False), (True, False, False), (True, True, False),
+                                   (True, True, True)):
+            st = Stack(fused=fused, silu=silu, chain=chain)
             per, _ = time_graph(st, 4, 1)
             d = {"us_per_token": round(per * 1e6, 2), "GB_s": round(st.algo_bytes / per / 1e9, 1),
                  "gemvs_per_token": len(st.layers), "algorithmic_bytes": st.algo_bytes,
                  "us_per_gemv": round(per * 1e6 / len(st.layers), 3)}
             name = "smollm2_135m_int4_g32_decode_stack" + ("_qkv_gateup_fused" if fused else "") + \
-                ("_silu_epilogue" if silu else "")
+                ("_silu_epilogue" if silu else "") + ("_chained" if chain else "")
             extra[name] = d
             log(name, d)
     if want("w8a16"):
