@@ -20,7 +20,7 @@
  *   - All pointers are device pointers.  The library allocates only a
  *     grow-only fp32 workspace per (device, stream), on the first prefill
  *     that splits K and on the first SiLU * mul call without a fused kernel;
- *     it is held until the process ends.
+ *     it is held until the process ends or locomp_amd_release_workspaces.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
  *     is asynchronous: the caller synchronises.
  *   - Return value: 0 on success; a negative LQ_ERR_* for invalid arguments
@@ -87,6 +87,14 @@ const char* locomp_amd_strerror(int code);
  * used by tests to run the shape-generic kernels on the same inputs. */
 int locomp_amd_set_policy(int policy);
 int locomp_amd_get_policy(void);
+
+/* Frees the fp32 workspaces the library keeps for `stream` on the current
+ * device (all streams of the device if all_streams != 0), including buffers
+ * superseded when a workspace grew; waits for the device to be idle first.
+ * The next call that needs a workspace allocates it again.  A HIP graph
+ * captured before the release that names one of them must not be replayed.
+ * No counterpart in the reference (which allocates nothing across calls). */
+int locomp_amd_release_workspaces(void* stream, int all_streams);
 
 /* Dequantize int4 -> OUT [N, K].
  * Replaces locomp_launch_dequant_int4 generated for

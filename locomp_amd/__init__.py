@@ -17,7 +17,7 @@ from .ops import (gpu_dequant_int4, gpu_dequant_int8, gpu_matvec_int4, gpu_matve
                   gpu_matvec_int8, interleave_gate_up)
 from .quantize import quantize_int4, quantize_int4_ref, quantize_int8
 from .checkpoint import QuantizedLinear, load_packed, quantize_checkpoint, read_packed, save_packed
-from ._lib import LocompAMDError, get_policy, set_policy
+from ._lib import LocompAMDError, get_policy, release_workspaces, set_policy
 
 __version__ = "0.1.0"
 
@@ -48,6 +48,6 @@ __all__ = [
     "gpu_matvec_int4_silu_mul", "interleave_gate_up",
     "quantize_int4", "quantize_int4_ref", "quantize_int8",
     "QuantizedLinear", "quantize_checkpoint", "save_packed", "read_packed", "load_packed",
-    "LocompAMDError", "set_policy", "get_policy",
+    "LocompAMDError", "set_policy", "get_policy", "release_workspaces",
     "Float16", "UInt8", "Int8", "Int32", "BFloat16", "constexpr",
 ]

@@ -34,6 +34,7 @@ SIGNATURES = {
     "locomp_amd_strerror": [_int],
     "locomp_amd_set_policy": [_int],
     "locomp_amd_get_policy": [],
+    "locomp_amd_release_workspaces": [_vp, _int],
     "locomp_amd_dequant_int4": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp],
     "locomp_amd_dequant_int8": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp],
     "locomp_amd_dequant_matvec_int4": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -100,3 +101,8 @@ def set_policy(policy: int) -> None:
 
 def get_policy() -> int:
     return load().locomp_amd_get_policy()
+
+
+def release_workspaces(stream=None, all_streams=True) -> None:
+    """Free the library's cached fp32 workspaces (see the C entry)."""
+    check(load().locomp_amd_release_workspaces(stream, 1 if all_streams else 0), "release_workspaces")

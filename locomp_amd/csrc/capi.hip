@@ -33,6 +33,7 @@ int launch_silu_fast(const void*, const void*, const void*, void*, int64_t, int6
 int launch_gemm_silu(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                      int64_t, int, int, hipStream_t);
 void* stream_workspace(int, size_t, hipStream_t);
+int release_workspaces(hipStream_t, bool);
 int launch_silu_pairs(const float*, void*, int64_t, int64_t, int, hipStream_t);
 int launch_generic_silu(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                         int64_t, int, int, int, hipStream_t);
@@ -135,6 +136,10 @@ int locomp_amd_set_policy(int policy) {
 }
 
 int locomp_amd_get_policy(void) { return g_policy.load(); }
+
+int locomp_amd_release_workspaces(void* stream, int all_streams) {
+  return release_workspaces(static_cast<hipStream_t>(stream), all_streams != 0);
+}
 
 int locomp_amd_dequant_int4(const void* W, const void* SCALES, void* OUT, int64_t K, int64_t HALF_K,
                             int64_t NUM_SCALES, int64_t GROUP_SIZE, int64_t N, int scale_dtype,

@@ -522,6 +522,7 @@ struct SplitWs {
 };
 static std::mutex g_ws_mu;
 static std::vector<SplitWs> g_ws;
+static std::vector<SplitWs> g_ws_old;   // superseded by a larger buffer (a graph may name them)
 
 void* stream_workspace(int slot, size_t bytes, hipStream_t st) {
   int dev = 0;
@@ -540,12 +541,42 @@ void* stream_workspace(int slot, size_t bytes, hipStream_t st) {
   }
   for (SplitWs& w : g_ws)
     if (w.dev == dev && w.st == st && w.slot == slot) {   // grown: the old buffer stays allocated
+      g_ws_old.push_back(w);
       w.p = p;
       w.bytes = sz;
       return p;
     }
   g_ws.push_back(SplitWs{dev, st, slot, p, sz});
   return p;
+}
+
+// Frees the workspaces kept for `st` on the current device (all streams of
+// the device if `all`), after waiting for the device to be idle.  A graph
+// captured earlier that names one must not be replayed afterwards.
+int release_workspaces(hipStream_t st, bool all) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return int(e);
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  bool any = false;
+  for (const auto* v : {&g_ws, &g_ws_old})
+    for (const SplitWs& w : *v) any = any || (w.dev == dev && (all || w.st == st));
+  if (!any) return LQ_OK;
+  e = hipDeviceSynchronize();
+  if (e != hipSuccess) return int(e);
+  for (auto* v : {&g_ws, &g_ws_old}) {
+    std::vector<SplitWs> keep;
+    for (const SplitWs& w : *v) {
+      if (w.dev == dev && (all || w.st == st)) {
+        e = hipFree(w.p);
+        if (e != hipSuccess) return int(e);
+      } else {
+        keep.push_back(w);
+      }
+    }
+    v->swap(keep);
+  }
+  return LQ_OK;
 }
 static void* split_workspace(size_t bytes, hipStream_t st) { return stream_workspace(0, bytes, st); }
 

@@ -354,6 +354,19 @@ def test_prefill_big_tiles_split_two(wbits):
     _close(got, _oracle(wbits, X, W, S, G))
 
 
+def test_release_workspaces_then_split_k_again():
+    """Freeing the cached split-K workspace (and the SiLU staging one) leaves
+    later calls correct: they allocate again."""
+    M, N, K, G = 128, 2048, 4096, 128
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=31)
+    first = _matvec(4, X, W, S, N, K, G, "f16")
+    lq.release_workspaces()
+    again = _matvec(4, X, W, S, N, K, G, "f16")
+    assert np.array_equal(first.view(np.uint16), again.view(np.uint16))
+    _close(again, _oracle(4, X, W, S, G))
+    lq.release_workspaces()
+
+
 def test_matmul_prefill_split_k_graph():
     """Split-K GEMM + reduction captured in a graph: every replay (with eager
     work and synchronisations between them) matches the eager result."""
