@@ -964,15 +964,23 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
         sv[r][c] = __builtin_amdgcn_raw_buffer_load_b32(rs, kin ? g * 4 : kSegOob, ((n0 + r) * num_scales) * 4, 0);
     }
   __builtin_amdgcn_sched_barrier(0);
-  // 3. weights
+  // 3. weights: the first kEarly chunks now, the rest after the operand
+  // barriers below.  A wave reaches a barrier only once it has issued every
+  // load before it, and issue stalls while the CU's memory queue is full, so
+  // issuing all weights here made each workgroup wait for its slowest issuer
+  // (operands ready 1.1-4.0 us after the start; 0.8-1.8 us this way).
+  constexpr int kEarly = 2;
   u32x4_t wv[RW][NSEG];
+  auto wload = [&](int r, int c) {
+    wv[r][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+        rw, !PART || c * 2048 + pos * 32 < K ? c * 1024 + pos * 16 : kSegOob, (n0 + r) * half_k,
+        2 /* nontemporal */));
+  };
 #pragma unroll
   for (int r = 0; r < RW; ++r)
 #pragma unroll
     for (int c = 0; c < NSEG; ++c)
-      wv[r][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-          rw, !PART || c * 2048 + pos * 32 < K ? c * 1024 + pos * 16 : kSegOob, (n0 + r) * half_k,
-          2 /* nontemporal */));
+      if (r * NSEG + c < kEarly) wload(r, c);
   __builtin_amdgcn_sched_barrier(0);
 
   // 4. activation operands and bias accumulators, built once per workgroup
@@ -1034,6 +1042,13 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
     }
   }
   __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c)
+      if (r * NSEG + c >= kEarly) wload(r, c);
+  __builtin_amdgcn_sched_barrier(0);
   u32x4_t xv[M_][NSEG][NP][4];
   float4_t negcorr[M_][NSEG];
 #pragma unroll
