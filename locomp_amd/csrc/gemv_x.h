@@ -66,8 +66,8 @@ static int launch_seg_x(const void* X, const void* W, const void* S, void* O, in
     else if (nseg <= 4) launch_seg_x_t<4, 2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
     else launch_seg_x_t<8, 1, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
   } else {
-    if (nseg == 1) launch_seg_x_t<1, 4, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
-    else if (nseg == 2) launch_seg_x_t<2, 2, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
+    if (nseg == 1) launch_seg_x_t<1, 8, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
+    else if (nseg == 2) launch_seg_x_t<2, 4, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
     else return LQ_ERR_SHAPE;
   }
   return check_launch();
