@@ -1,0 +1,171 @@
+// gemv_rows_kernel: row-contiguous int4 decode GEMV (M <= 2, G % 32), with the SiLU * mul epilogue.
+// Part of the decode GEMV kernels; see gemv_impl.h for the kernel choice.
+#pragma once
+#include "gemv_common.h"
+
+namespace lq {
+
+// ------------------------------------------ decode GEMV, row-contiguous --
+// int4, M <= 2.  Each wave owns RW whole weight rows; lane l covers the 32 k
+// starting at c * 2048 + 32 * l of every row (segment c < NSEG), so each wave
+// load instruction reads 1 KB contiguous of one row.  The lane's activations
+// for its k-range are loaded once (k-permuted to match the decoder) and reused
+// for all RW rows; their sum is kept to remove the decoder's +1032 bias.  Per
+// 16 bytes of weights: 7 VALU ops decode 4 x 8 weights to biased fp16 pairs,
+// 16 v_dot2_f32_f16 accumulate in fp32, and the 32-k partial is un-biased and
+// scaled (the 32 k lie in one group).  Rows are reduced across the wave with a
+// transposed butterfly (log2(RW) exchange stages, then 6 - log2(RW) plain
+// stages).  Load order: activations, scales, then all weights, so the
+// in-order vmcnt lets each row start as soon as its own bytes arrive.
+// EPI: the weight rows are gate / up interleaved (row 2i = gate_i, 2i + 1 =
+// up_i) and the kernel stores silu(gate_i) * up_i to O [M, N / 2] instead of
+// the N dot products (examples/54_smollm2_inference.py:113-120, 545-548).
+template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false>
+__global__ __launch_bounds__(256, 3) void gemv_rows_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
+  typedef typename Elem<SD>::T stype;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * RW;
+  const int half_k = K >> 1;
+
+  // 1. activations (k-permuted) for this lane's k-ranges
+  u32x4_t xv[M_][NSEG][4];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + lane * 32, K - 32);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xv[m][c][e] = *reinterpret_cast<const u32x4_t*>(X + size_t(m < M ? m : 0) * K + k0 + e * 8);
+    }
+  // 2. scales of (row, segment)
+  const stype* sp = static_cast<const stype*>(S);
+  stype sv[RW][NSEG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + lane * 32, K - 32);
+      const int n = min(n0 + r, N - 1);
+      sv[r][c] = sp[size_t(n) * num_scales + k0 / group];
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. all weights of this wave
+  u32x4_t wv[RW][NSEG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + lane * 32, K - 32);
+      const int n = min(n0 + r, N - 1);
+      wv[r][c] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(W + size_t(n) * half_k + (k0 >> 1)));
+    }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. permute activations, bias correction per (m, segment)
+  const half2_t ones = {half_t(1.f), half_t(1.f)};
+  float corr[M_][NSEG];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xv[m][c][e] = xperm8(xv[m][c][e]);
+        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].x), ones, sum, false);
+        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].y), ones, sum, false);
+        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].z), ones, sum, false);
+        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].w), ones, sum, false);
+      }
+      const bool valid = (m < M) && (c * 2048 + lane * 32 < K);
+      corr[m][c] = valid ? sum * kInt4Bias : 0.f;
+    }
+
+  // 5. rows
+  float acc[M_][RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int m = 0; m < M_; ++m) acc[m][r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const bool valid = c * 2048 + lane * 32 < K;
+      // four independent dot2 chains (one per dword) keep the VALU pipeline
+      // busy instead of waiting on one 16-long accumulate chain
+      float pe[M_][4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const u32x4_t b = int4x8_biased_kperm(wv[r][c][e]);
+#pragma unroll
+        for (int m = 0; m < M_; ++m) {
+          float t = __builtin_amdgcn_fdot2(as_h2(b.x), as_h2(xv[m][c][e].x), 0.f, false);
+          t = __builtin_amdgcn_fdot2(as_h2(b.y), as_h2(xv[m][c][e].y), t, false);
+          t = __builtin_amdgcn_fdot2(as_h2(b.z), as_h2(xv[m][c][e].z), t, false);
+          pe[m][e] = __builtin_amdgcn_fdot2(as_h2(b.w), as_h2(xv[m][c][e].w), t, false);
+        }
+      }
+      float part[M_];
+#pragma unroll
+      for (int m = 0; m < M_; ++m) part[m] = (pe[m][0] + pe[m][1]) + (pe[m][2] + pe[m][3]);
+      float sc;
+      if constexpr (SD == LQ_F32) sc = sv[r][c];
+      else if constexpr (SD == LQ_F16) sc = float(sv[r][c]);
+      else sc = bf16_to_f32(sv[r][c]);
+      sc = valid ? sc : 0.f;
+#pragma unroll
+      for (int m = 0; m < M_; ++m) acc[m][r] += (part[m] - corr[m][c]) * sc;
+      // consume in load order: no hoisting of later rows' decode (register
+      // pressure) and no early waits on their loads
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // 6. reduce each row over the 64 lanes: transposed butterfly
+#pragma unroll
+  for (int m = 0; m < M_; ++m) {
+    float v[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) v[r] = acc[m][r];
+    int cnt = RW;
+    int width = 32;
+#pragma unroll
+    for (; cnt > 1; cnt >>= 1, width >>= 1) {
+      const bool upper = (lane & width) != 0;
+      const int h = cnt >> 1;
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float keep = upper ? v[i + h] : v[i];
+        const float send = upper ? v[i] : v[i + h];
+        v[i] = keep + __shfl_xor(send, width, 64);
+      }
+    }
+#pragma unroll
+    for (; width > 0; width >>= 1) v[0] += __shfl_xor(v[0], width, 64);
+    // lane bits 5..(6 - log2 RW) name the row
+    int row = 0;
+    {
+      int w2 = 32;
+#pragma unroll
+      for (int c2 = RW; c2 > 1; c2 >>= 1, w2 >>= 1) row = row * 2 + ((lane & w2) ? 1 : 0);
+    }
+    const int lowmask = (64 / RW) - 1;
+    if constexpr (EPI) {
+      static_assert(RW % 2 == 0, "gate / up pairs within one wave");
+      // row r and r ^ 1 sit in lanes that differ in bit log2(64 / RW)
+      const float other = __shfl_xor(v[0], 64 / RW, 64);
+      if ((lane & lowmask) == 0 && (row & 1) == 0 && m < M && n0 + row + 1 < N) {
+        const float g = v[0];
+        store_f32<OD>(O, size_t(m) * (N >> 1) + ((n0 + row) >> 1), g / (1.0f + expf(-g)) * other);
+      }
+    } else {
+      if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+    }
+  }
+}
+
+}  // namespace lq
