@@ -257,7 +257,8 @@ static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, 
                                        : (G >= span && eighth_k % G == 0);
   // (a partial last chunk only behind >= 4 whole ones: on shorter rows the
   // row / LDS kernels are faster)
-  return M >= 1 && M <= 16 && row_bytes >= kTChunkB && row_bytes % 16 == 0 && groups_ok &&
+  return M >= 1 && M <= 16 && K < (int64_t(1) << 22) && row_bytes >= kTChunkB &&
+         row_bytes % 16 == 0 && groups_ok &&
          (row_bytes % kTChunkB == 0 || row_bytes >= 4 * kTChunkB) &&
          N * row_bytes < (int64_t(1) << 31) &&
          (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_count(N, K, G, scale_bytes) > 0;
@@ -277,7 +278,7 @@ static int gemv_tile_xl_count(int wbits, int64_t N, int64_t K, int64_t G, int sc
   return tiles;
 }
 static bool gemv_tile_xl_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, int scale_bytes) {
-  return M > 16 && M <= 64 && K % kXChunkK == 0 && G % 32 == 0 &&
+  return M > 16 && M <= 64 && K % kXChunkK == 0 && K < (int64_t(1) << 22) && G % 32 == 0 &&
          (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_xl_count(wbits, N, K, G, scale_bytes) > 0;
 }
 template <int WBITS, int SD, int OD, bool EPI = false>

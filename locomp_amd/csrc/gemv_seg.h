@@ -35,6 +35,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   constexpr int kXB = XD == LQ_F32 ? 4 : 2;    // activation element bytes
   const int sd = SD == kRT ? sd_rt : SD;
   const int ssz = sd == LQ_F32 ? 4 : 2;
+  const float rgroup = 1.0f / float(group);    // for div_rcp (K <= 16384 here)
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * 4 + wave) * RW;
@@ -74,7 +75,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 #pragma unroll
     for (int c = 0; c < NSEG; ++c) {
       const bool kin = !PART || c * 2048 + pos * 32 < K;
-      const int g = (c * 2048 + pos * 32) / group;
+      const int g = div_rcp(c * 2048 + pos * 32, group, rgroup);
       if (ssz == 2)
         sv[r][c] = __builtin_amdgcn_raw_buffer_load_b16(rs, kin ? g * 2 : kSegOob, ((n0 + r) * num_scales) * 2, 0);
       else

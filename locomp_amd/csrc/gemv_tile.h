@@ -60,6 +60,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   typedef TileMfma<WBITS, XD> Mf;
   typedef typename Mf::op_t op_t;
   typedef typename Mf::x_t x_t;
+  const float rgroup = 1.0f / float(group);             // for div_rcp (K < 2^22)
   constexpr int kSpan = Mf::kSpan;                      // k per MFMA block
   constexpr int kEighthK = kTBlocks * kSpan;            // k per wave per chunk
   constexpr int kChunkK = kTWaves * kEighthK;
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
       }
 #pragma unroll
       for (int sg = 0; sg < NSC; ++sg) {
-        int g = (kbase + sg * kPerScale * kSpan) / group;
+        int g = div_rcp(kbase + sg * kPerScale * kSpan, group, rgroup);
         if constexpr (PART) g = min(g, num_scales - 1);
         sc[t][sg] = load_scale<SD>(sl + (size_t(row) * num_scales + g) * kSSize, sd_rt);
       }
@@ -331,9 +332,12 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
 // the chunk's DMA instructions are dealt round-robin over the 8 waves, every
 // load is a DMA, so a step's wait is a bare vmcnt of this wave's count.  Wave
 // w takes k [32 w, 32 w + 32) of the chunk for all 4 x T (activation x
-// weight) tiles: int8 two exact 16x16x16 blocks; int4 one 16x16x32 block
-// with the 5-op biased decode, the bias one MFMA per activation tile shared
-// by the T weight tiles.  The group scale (G % 32 == 0) is applied in fp32.
+// weight) tiles as one 16x16x32 block: int8 weights converted to fp16
+// exactly, summed raw over the chunks of a scale group and scaled when the
+// group changes; int4 with the 5-op biased decode, the bias one MFMA per
+// activation tile shared by the T weight tiles, scaled every chunk.  The
+// group scale (G % 32 == 0) is applied in fp32.  Workgroup b walks the
+// chunks starting at chunk b mod (K / 256).
 constexpr int kXChunkK = 256;
 constexpr int kXSlots = 3;
 // LDS of the ring (also the cross-wave sum) and of the scale rows: whatever
@@ -354,6 +358,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
   typedef TileMfma<WBITS> Mf;
   typedef typename Mf::op_t op_t;
+  const float rgroup = 1.0f / float(group);             // for div_rcp (K < 2^22)
   constexpr int kRows = 16 * TILES;
   constexpr int kRowB = kXChunkK * WBITS / 8;             // weight bytes per row per chunk
   constexpr int kPos = kRowB / 16;                        // 16-byte positions per weight row
@@ -375,7 +380,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (SGPR)
   const int r16 = lane & 15;
   const int q4 = lane >> 4;
   const int n0 = blockIdx.x * kRows;
@@ -407,12 +412,17 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
       dst[i] = kWBytes + (j - kWInstr) * 1024;
     }
   }
+  // Step c works on chunk phys(c): workgroup b starts at chunk b mod nchunks,
+  // so the workgroups do not all read the same column of their rows at once.
+  const int rot = int(blockIdx.x % unsigned(nchunks));
+  auto phys = [&](int c) { const int p = c + rot; return p >= nchunks ? p - nchunks : p; };
   auto issue = [&](int slot, int c) {
     uint8_t* base = &ring[slot * kSlotB];
+    const int pc = phys(c);
 #pragma unroll
     for (int i = 0; i < kPerWaveMax; ++i)
       if (i < my_count)
-        dma16(src[i] + size_t(c) * (is_w[i] ? kRowB : kXChunkK * 2), base + dst[i]);
+        dma16(src[i] + size_t(pc) * (is_w[i] ? kRowB : kXChunkK * 2), base + dst[i]);
   };
   // wait until at most `groups` of this wave's chunk groups are outstanding
   // (a wave issues kPerWaveMax or kPerWaveMax - 1 DMAs per chunk)
@@ -445,40 +455,76 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
 #pragma unroll
     for (int t = 0; t < TILES; ++t) acc[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
 
+  // int8: raw sums over the chunks of one scale group, scaled into acc when
+  // the group changes (per-channel scales: once, after the last chunk).
+  float4_t raw[4][TILES];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) raw[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  auto add_scaled = [&](const float4_t (&part)[4][TILES], int g) {
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const uint8_t* ps = sl + (size_t(t * 16 + r16) * num_scales + g) * kSSize;
+      float sc;
+      if constexpr (SD == LQ_F32) sc = *reinterpret_cast<const float*>(ps);
+      else if constexpr (SD == LQ_F16) sc = float(*reinterpret_cast<const half_t*>(ps));
+      else sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        acc[mt][t] += part[mt][t] * sc;
+        // keep the MFMA-result read in this block (see gemv_tile_kernel)
+        __asm__ volatile("" : "+v"(acc[mt][t]));
+      }
+    }
+  };
+
+  // int8: a group of G % 256 == 0 spans cpg whole chunks (and the chunk walk
+  // wraps at a group boundary, K % G == 0); other groups are scaled every
+  // chunk.  `left` counts the chunks to the end of the current group.
+  const int cpg = group % kXChunkK == 0 ? group / kXChunkK : 1;
+  int left = cpg - rot % cpg;
   auto compute = [&](int slot, int c) {
     const uint8_t* wl = &ring[slot * kSlotB];
     const uint8_t* xl = wl + kWBytes;
-    float4_t part[4][TILES];
+    const int pc = phys(c);
     if constexpr (WBITS == 8) {
+      // one 16x16x32 block: the lane's 8 k are wave * 32 + q4 * 8 ..: bytes
+      // 8 q4 of weight position 2 wave + q4 / 2, activation position 4 wave + q4;
+      // the int8 weights are converted to fp16 exactly.
+      h8 bw[TILES];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int t = 0; t < TILES; ++t) {
+        const int row = t * 16 + r16;
+        const u32x2_t w = *reinterpret_cast<const u32x2_t*>(
+            wl + row * kRowB + (((2 * wave + (q4 >> 1)) ^ (row & (kPos - 1))) << 4) + ((q4 & 1) << 3));
+        half2_t lo[2], hi[2];
+        int8x4_to_h2(w.x, lo);
+        int8x4_to_h2(w.y, hi);
+        bw[t] = h8{lo[0][0], lo[0][1], lo[1][0], lo[1][1], hi[0][0], hi[0][1], hi[1][0], hi[1][1]};
+      }
 #pragma unroll
-        for (int t = 0; t < TILES; ++t) part[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = mt * 16 + r16;
+        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(
+            xl + row * (kXChunkK * 2) + (((4 * wave + q4) ^ (row & 15)) << 4));
+        const h8 xa = __builtin_bit_cast(h8, xv);
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        const int kb = wave * 32 + f * 16 + q4 * 4;          // this lane's 4 k (= bytes)
-        op_t bw[TILES];
+        for (int t = 0; t < TILES; ++t)
+          raw[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bw[t], raw[mt][t], 0, 0, 0);
+      }
+      if (--left == 0 || c + 1 == nchunks) {
+        left = cpg;
+        add_scaled(raw, div_rcp(pc * kXChunkK + wave * 32, group, rgroup));
 #pragma unroll
-        for (int t = 0; t < TILES; ++t) {
-          const int row = t * 16 + r16;
-          const uint32_t w = *reinterpret_cast<const uint32_t*>(
-              wl + row * kRowB + (((kb >> 4) ^ (row & (kPos - 1))) << 4) + (kb & 15));
-          bw[t] = Mf::decode(w, magic);
-        }
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const int row = mt * 16 + r16;
-          const int byte = kb * 2;
-          const u32x2_t xv = *reinterpret_cast<const u32x2_t*>(
-              xl + row * (kXChunkK * 2) + (((byte >> 4) ^ (row & 15)) << 4) + (byte & 15));
-          const op_t xa = Mf::prep_x(xv);
-#pragma unroll
-          for (int t = 0; t < TILES; ++t) part[mt][t] = Mf::mfma(xa, bw[t], part[mt][t]);
-        }
+          for (int t = 0; t < TILES; ++t) raw[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
       }
     } else {
       // one 16x16x32 block: the lane's 8 k are wave * 32 + q4 * 8 .., i.e.
       // dword q4 of weight chunk `wave` and activation bytes 64 w + 16 q4
+      float4_t part[4][TILES];
       op_t bw[TILES];
 #pragma unroll
       for (int t = 0; t < TILES; ++t) {
@@ -499,21 +545,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
 #pragma unroll
         for (int t = 0; t < TILES; ++t) part[mt][t] = Mf::mfma(xa, bw[t], start);
       }
-    }
-    const int g = (c * kXChunkK + wave * 32) / group;
-#pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-      const uint8_t* ps = sl + (size_t(t * 16 + r16) * num_scales + g) * kSSize;
-      float sc;
-      if constexpr (SD == LQ_F32) sc = *reinterpret_cast<const float*>(ps);
-      else if constexpr (SD == LQ_F16) sc = float(*reinterpret_cast<const half_t*>(ps));
-      else sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        acc[mt][t] += part[mt][t] * sc;
-        // keep the MFMA-result read in this block (see gemv_tile_kernel)
-        __asm__ volatile("" : "+v"(acc[mt][t]));
-      }
+      add_scaled(part, div_rcp(pc * kXChunkK + wave * 32, group, rgroup));
     }
   };
 

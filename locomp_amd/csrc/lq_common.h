@@ -163,6 +163,19 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t o
   return (x & mask) | orv;
 }
 
+// a / d for 0 <= a < 2^22 and d >= 1, given rd = 1.0f / d.  The float
+// product is within 0.75 of a / d (two roundings of at most 2^-24 relative
+// each, a / d < 2^22), so its truncation is off by at most one, and the
+// remainder test corrects that.  A few VALU ops instead of the integer
+// division sequence.
+__device__ __forceinline__ int div_rcp(int a, int d, float rd) {
+  int q = int(float(a) * rd);
+  const int r = a - q * d;
+  q += r >= d ? 1 : 0;
+  q -= r < 0 ? 1 : 0;
+  return q;
+}
+
 // A value the optimiser cannot constant-fold (held in a VGPR).
 __device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
   __asm__ volatile("" : "+v"(v));

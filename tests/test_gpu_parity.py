@@ -194,10 +194,15 @@ def test_matvec_lds_ring_shapes(wbits, M, N, K, G):
 @pytest.mark.parametrize("wbits", [4, 8])
 @pytest.mark.parametrize("M,N,K,G", [
     (17, 64, 1024, 64), (33, 300, 2048, 16), (64, 1000, 4096, 4096), (48, 4100, 1536, 512),
-    (16, 1000, 4096, 4096), (3, 77, 1024, 1024), (32, 11008, 4096, 128), (64, 9000, 768, 32)])
+    (16, 1000, 4096, 4096), (3, 77, 1024, 1024), (32, 11008, 4096, 128), (64, 9000, 768, 32),
+    (40, 500, 1536, 384), (24, 333, 3072, 768), (64, 14336, 4096, 4096)])
 def test_matvec_many_rows_and_per_channel(wbits, M, N, K, G):
     """Decode/verify sizes up to M = 64 and per-channel / large groups
-    (one or few scales per row, whose scale rows are not 16-byte multiples)."""
+    (one or few scales per row, whose scale rows are not 16-byte multiples).
+    At 16 < M <= 64 the int8 kernel sums whole-chunk groups (G % 256 == 0:
+    768 = 3 chunks, per-channel) before scaling and scales other groups
+    (384, 128, ...) every chunk; each workgroup starts at a different chunk,
+    so the group walks wrap."""
     if wbits == 4 and G % 32:
         pytest.skip("int4 groups hold whole 32-k lane spans")
     X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=3 * M + N + K)
