@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   const int ssz = sd == LQ_F32 ? 4 : 2;
   const float rgroup = 1.0f / float(group);    // for div_rcp (K <= 16384 here)
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (SGPR)
   const int n0 = (blockIdx.x * 4 + wave) * RW;
   const int half_k = K >> 1;
   const int j = lane & 15, q = lane >> 4;
@@ -182,11 +182,14 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 
   // 5. rows: decode (5 ops / 8 weights) + MFMA, chains start at -bias
   const uint32_t magic = opaque_u32(kH ? 0x64006400u : 0x43004300u);
-  float acc[M_][RW];
+  // acc4 keeps all four MFMA result registers scaled by the lane's scale;
+  // only element dreg (the lane's diagonal entry) is used, picked once per
+  // row after the last segment (a per-segment pick compiles to branches).
+  float4_t acc4[M_][RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
 #pragma unroll
-    for (int m = 0; m < M_; ++m) acc[m][r] = 0.f;
+    for (int m = 0; m < M_; ++m) acc4[m][r] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NSEG; ++c) {
       float4_t d[M_];
@@ -222,12 +225,20 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
       else if (sd == LQ_F16) sc = float(__builtin_bit_cast(half_t, uint16_t(sv[r][c])));
       else sc = bf16_to_f32(uint16_t(sv[r][c]));
 #pragma unroll
-      for (int m = 0; m < M_; ++m) {
-        const float dv = dreg == 0 ? d[m][0] : dreg == 1 ? d[m][1] : dreg == 2 ? d[m][2] : d[m][3];
-        acc[m][r] += dv * sc;
-      }
+      for (int m = 0; m < M_; ++m) acc4[m][r] += d[m] * sc;
     }
   }
+  float acc[M_][RW];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      float dv = acc4[m][r][0];
+      dv = dreg == 1 ? acc4[m][r][1] : dv;
+      dv = dreg == 2 ? acc4[m][r][2] : dv;
+      dv = dreg == 3 ? acc4[m][r][3] : dv;
+      acc[m][r] = dv;
+    }
 
   // 6. reduce each row over the 16 diagonal lanes
 #pragma unroll
