@@ -18,7 +18,7 @@ int launch_gemm_x(const void*, const void*, const void*, void*, int64_t, int64_t
                   int, int, int, hipStream_t, const FixedScratch*);
 template <int WBITS>
 int launch_skinny_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
-                    int64_t, int, int, int, hipStream_t);
+                    int64_t, int, int, int, hipStream_t, const FixedScratch*);
 template <int WBITS>
 int launch_generic(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
                    int, int, int, hipStream_t);
@@ -81,7 +81,7 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
                            aligned(S, 4) && K % 8 == 0;
   if (fast_common && (xd == LQ_BF16 || xd == LQ_F32) && M <= 16) {
     // bf16 activations (M <= 16) and fp32 (M <= 4) on bf16 MFMAs
-    const int rc = launch_skinny_x<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st);
+    const int rc = launch_skinny_x<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st, fixed);
     if (rc != LQ_ERR_SHAPE) return rc;
   }
   if (fast_common && xd == LQ_BF16 && M > 16 && K % 64 == 0) {

@@ -49,15 +49,17 @@ __device__ __forceinline__ void dma16_buf(i32x4_t rsrc, uint32_t voff, const voi
 // EPI = gate/up rows interleaved (2i, 2i + 1): store silu(gate) * up to
 // O [M, N / 2] instead of O [M, N].
 // XD = activation dtype (fp16, bf16, or fp32 for M <= 4: MFMA row
-// m + 4 part holds part `part` of activation row m); SD / OD = kRT take the
-// scale / output dtype from sd_rt / od_rt.
+// m + 4 part holds part `part` of activation row m; kXPre: the same rows
+// read as bf16 from a matrix of parts split beforehand); SD / OD = kRT take
+// the scale / output dtype from sd_rt / od_rt.
 template <int WBITS, int NSC, int TILES, int SD, int OD, bool PART, bool EPI = false,
           int XD = LQ_F16>
 __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
     const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
     int od_rt = 0) {
-  typedef TileMfma<WBITS, XD> Mf;
+  constexpr bool kPre = XD == kXPre;                     // pre-split fp32: bf16 part rows
+  typedef TileMfma<WBITS, kPre ? LQ_BF16 : XD> Mf;
   typedef typename Mf::op_t op_t;
   typedef typename Mf::x_t x_t;
   const float rgroup = 1.0f / float(group);             // for div_rcp (K < 2^22)
@@ -66,7 +68,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   constexpr int kChunkK = kTWaves * kEighthK;
   constexpr int kPerScale = kTBlocks / NSC;             // blocks sharing one scale
   constexpr int kXB = XD == LQ_F32 ? 4 : 2;             // activation element bytes
-  constexpr bool kSplit = XD == LQ_F32;
+  constexpr bool kSplit = XD == LQ_F32 || kPre;        // MFMA row m + 4 part
   const int kSSize = scale_size<SD>(sd_rt);
   constexpr int kRows = 16 * TILES;
   constexpr int kDma = TILES;                           // DMA instructions per wave per chunk
@@ -128,8 +130,9 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
   // (fp32: MFMA row r16 = m + 4 part, m = r16 % 4)
   const int xm = kSplit ? (r16 & 3) : r16;
   const int xpart = kSplit ? (r16 >> 2) : 0;
+  // (pre-split: lane row r16 is row r16 of the part matrix)
   const uint8_t* xrow = static_cast<const uint8_t*>(X) +
-                        (size_t(min(xm, M - 1)) * K + wave * kEighthK + q4 * (kSpan / 4)) * kXB;
+                        (size_t(kPre ? r16 : min(xm, M - 1)) * K + wave * kEighthK + q4 * (kSpan / 4)) * kXB;
   struct Batch {
     x_t x[kTBlocks];
   };
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
     op_t xa[kTBlocks];
 #pragma unroll
     for (int f = 0; f < kTBlocks; ++f) {
-      xa[f] = Mf::prep_x(bt.x[f], xpart);
+      xa[f] = Mf::prep_x(bt.x[f], kPre ? 0 : xpart);
       if (PART && kbase + f * kSpan + q4 * (kSpan / 4) >= K) xa[f] = op_t{};
     }
 #pragma unroll

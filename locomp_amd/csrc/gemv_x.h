@@ -6,6 +6,33 @@
 
 namespace lq {
 
+void* stream_workspace(int slot, size_t bytes, hipStream_t st);
+
+// fp32 activations X [M, K] (M <= 4) -> their exact three-way bf16 split,
+// P [12, K] bf16 with row m + 4 part = part `part` of row m (rows of m >= M
+// are not written; the tile kernel does not read them).  Thread i takes 8
+// consecutive k of one row.
+static __global__ __launch_bounds__(256) void split_f32_parts_kernel(const float* __restrict__ X,
+                                                             uint16_t* __restrict__ P, int M,
+                                                             int K) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int per_row = K >> 3;
+  if (i >= M * per_row) return;
+  const int m = i / per_row, k = (i - m * per_row) * 8;
+  const u32x4_t a = *reinterpret_cast<const u32x4_t*>(X + size_t(m) * K + k);
+  const u32x4_t b = *reinterpret_cast<const u32x4_t*>(X + size_t(m) * K + k + 4);
+  const uint32_t x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = f32_part_bits(x[e], p) >> 16;
+    const u32x4_t v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                       h[6] | (h[7] << 16)};
+    *reinterpret_cast<u32x4_t*>(P + size_t(m + 4 * p) * K + k) = v;
+  }
+}
+
 template <int WBITS, int XD, int NSC>
 static void launch_tile_x_nsc(const void* X, const void* W, const void* S, void* O, int64_t M,
                               int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
@@ -13,6 +40,7 @@ static void launch_tile_x_nsc(const void* X, const void* W, const void* S, void*
   // (3 and 4 spill)
   int tiles = gemv_tile_count(N, K, G, sd == LQ_F32 ? 4 : 2);
   if (XD == LQ_F32 && tiles > 2) tiles = 2;
+  // (the pre-split parts are bf16 rows: any tile count)
   const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
   const bool part = ((WBITS == 4 ? K / 2 : K) % kTChunkB) != 0;
 #define LQ_TX_LAUNCH(T_)                                                                        \
@@ -75,10 +103,15 @@ static int launch_seg_x(const void* X, const void* W, const void* S, void* O, in
 
 // bf16 activations at M <= 16, fp32 at M <= 4 (three MFMA rows per
 // activation row), on the shapes gemv_tile_ok accepts; LQ_ERR_SHAPE otherwise.
-// int4 M = 1 with G % 128 takes the segment kernel.
+// int4 M = 1 with G % 128 takes the segment kernel.  fp32 activations are
+// first split into bf16 part rows (split_f32_parts_kernel) in `fixed` or the
+// stream's workspace slot 2, so the tile kernel streams bf16 operands; with
+// neither available (a capturing stream before any such call) the tile
+// kernel splits them itself, at fewer tiles per workgroup.
 template <int WBITS>
 int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
-                    int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
+                    int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st,
+                    const FixedScratch* fixed) {
   if (xd != LQ_BF16 && xd != LQ_F32) return LQ_ERR_SHAPE;
   if constexpr (WBITS == 4) {
     const int rc = launch_seg_x(X, W, S, O, M, N, K, G, xd, sd, od, st);
@@ -94,7 +127,22 @@ int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_
     case 2: launch_tile_x_nsc<WBITS, XD_, 2>(X, W, S, O, M, N, K, G, sd, od, st); break;    \
     default: launch_tile_x_nsc<WBITS, XD_, 4>(X, W, S, O, M, N, K, G, sd, od, st); break;   \
   }
-  if (xd == LQ_BF16) { LQ_NSC(LQ_BF16) } else { LQ_NSC(LQ_F32) }
+  void* parts = nullptr;
+  if (xd == LQ_F32) {
+    const size_t bytes = size_t(12) * size_t(K) * 2;
+    parts = fixed ? (bytes <= fixed->bytes ? fixed->p : nullptr) : stream_workspace(2, bytes, st);
+  }
+  if (parts) {
+    const int threads = int(M * (K / 8));
+    hipLaunchKernelGGL(split_f32_parts_kernel, dim3((threads + 255) / 256), dim3(256), 0, st,
+                       static_cast<const float*>(X), static_cast<uint16_t*>(parts), int(M), int(K));
+    X = parts;
+    LQ_NSC(kXPre)
+  } else if (xd == LQ_BF16) {
+    LQ_NSC(LQ_BF16)
+  } else {
+    LQ_NSC(LQ_F32)
+  }
 #undef LQ_NSC
   return check_launch();
 }

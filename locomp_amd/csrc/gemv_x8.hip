@@ -3,5 +3,6 @@
 
 namespace lq {
 template int launch_skinny_x<8>(const void*, const void*, const void*, void*, int64_t, int64_t,
-                                int64_t, int64_t, int, int, int, hipStream_t);
+                                int64_t, int64_t, int, int, int, hipStream_t,
+                                const FixedScratch*);
 }  // namespace lq

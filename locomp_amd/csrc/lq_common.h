@@ -68,6 +68,10 @@ __device__ __forceinline__ void store_f32(void* p, size_t i, float v) {
 // the instantiations for bf16 and fp32 activations use it to bound their
 // number.
 constexpr int kRT = -1;
+// Activation code of the decode tile kernel for fp32 activations split
+// beforehand into their three exact bf16 parts: a bf16 matrix of 12 rows,
+// row m + 4 part = part `part` of activation row m (M <= 4).
+constexpr int kXPre = 100;
 template <int SD>
 __device__ __forceinline__ int scale_size(int sd_rt) {
   const int sd = SD == kRT ? sd_rt : SD;

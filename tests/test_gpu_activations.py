@@ -165,3 +165,60 @@ def test_fp32_split_is_exact_on_hard_values():
     scale = np.abs(X.astype(np.float64)).sum()
     # one bf16 part would err by ~2^-9 of the largest terms (~1e-3 of scale)
     assert np.abs(got - want).max() <= 2e-5 * scale
+
+
+def test_fp32_split_is_exact_on_hard_values_m3():
+    """The same at M = 3 (the rows are split into bf16 part rows by a separate
+    kernel first): row m of X scaled by 2^m, one weight row of ones."""
+    rng = np.random.default_rng(6)
+    K, N, G, M = 2048, 32, 2048, 3
+    X = (rng.standard_normal((M, K)) * np.exp2(rng.integers(-20, 20, (M, K)))).astype(np.float32)
+    W = np.full((N, K), 1, np.int8)
+    S = np.ones((N, 1), np.float32)
+    got = _run(8, X, W, S, N, K, G, "f32", "f32", "f32")
+    for m in range(M):
+        want = X[m].astype(np.float64).sum()
+        assert np.abs(got[m] - want).max() <= 2e-5 * np.abs(X[m].astype(np.float64)).sum()
+
+
+def test_fp32_activations_in_graph_on_a_fresh_stream():
+    """A capture on a stream with no workspace yet cannot allocate the part
+    rows: the tile kernel then splits the activations itself (a new torch
+    stream normally has none; a pooled one reused from an earlier fp32 call
+    would run the pre-split path inside the graph instead).  The graph is
+    replayed three times with eager calls on the default stream in between;
+    every replay must match the oracle (rtol 1e-4)."""
+    import ctypes
+
+    import torch
+
+    from locomp_amd import _lib
+
+    lib = _lib.load()
+    vp = ctypes.c_void_p
+    M, N, K, G = 3, 2000, 4096, 128
+    X, W, S = _case(4, M, N, K, G, seed=77)
+    want = _oracle(4, X, W, S, G)
+    Xd, Wd, Sd = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (X, W, S))
+    Od = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    Oe = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+
+    def call(out, stream):
+        return lib.locomp_amd_dequant_matvec_int4(
+            vp(Xd.data_ptr()), vp(Wd.data_ptr()), vp(Sd.data_ptr()), vp(out.data_ptr()), K, K // 2,
+            K // G, G, N, M, _lib.F32, _lib.F32, _lib.F32, vp(stream.cuda_stream))
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        assert call(Od, s) == 0
+    torch.cuda.synchronize()
+    for _ in range(3):
+        Od.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert call(Oe, torch.cuda.current_stream()) == 0   # eager work between replays
+        torch.cuda.synchronize()
+        _close32(Od.cpu().numpy(), want)
+        _close32(Oe.cpu().numpy(), want)

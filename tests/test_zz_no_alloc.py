@@ -3,9 +3,10 @@
 (locomp_amd_dequant_matvec_int4), through the C ABI on the same inputs.
 
 Both run the same kernels; the split-K prefill partials of the first live in
-the library's fixed per-GPU scratch array, so the outputs must be bit-identical,
-including on a second, smaller call right after the first (the array keeps the
-first call's contents)."""
+the library's fixed per-GPU scratch array (as do the bf16 part rows of fp32
+activations at M <= 4), so the outputs must be bit-identical, including on a
+second, smaller call right after the first (the array keeps the first call's
+contents)."""
 
 import ctypes
 
@@ -20,12 +21,13 @@ torch = pytest.importorskip("torch")
 vp = ctypes.c_void_p
 
 
-def _run(fn, X, W, S, M, N, K, G):
+def _run(fn, X, W, S, M, N, K, G, xd=None):
     stream = torch.cuda.current_stream()
     Xd, Wd, Sd = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (X, W, S))
     Od = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
     rc = fn(vp(Xd.data_ptr()), vp(Wd.data_ptr()), vp(Sd.data_ptr()), vp(Od.data_ptr()),
-            K, K // 2, K // G, G, N, M, _lib.F16, _lib.F16, _lib.F16, vp(stream.cuda_stream))
+            K, K // 2, K // G, G, N, M, _lib.F16 if xd is None else xd, _lib.F16, _lib.F16,
+            vp(stream.cuda_stream))
     torch.cuda.synchronize()
     return rc, Od.cpu().numpy()
 
@@ -47,6 +49,23 @@ def test_noalloc_matches_allocating_entry(first, second):
         X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=seed)
         rc_a, want = _run(lib.locomp_amd_dequant_matvec_int4, X, W, S, M, N, K, G)
         rc_b, got = _run(lib.locomp_amd_dequant_matvec_int4_noalloc, X, W, S, M, N, K, G)
+        assert rc_a == 0 and rc_b == 0, (rc_a, rc_b)
+        assert not np.isnan(got).any()
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_noalloc_fp32_activations_matches_allocating_entry():
+    """fp32 activations at 2 <= M <= 4 are split into bf16 part rows first:
+    in the fixed array here, in the stream's workspace for the allocating
+    entry.  The second call has fewer rows, so the array still holds the first
+    call's part rows past it; they must not be read."""
+    lib = _lib.load()
+    for seed, (M, N, K, G) in enumerate(((4, 11008, 4096, 128), (2, 3000, 2048, 64))):
+        print(f"noalloc fp32 case M={M} N={N} K={K} G={G}", flush=True)
+        X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=10 + seed)
+        X = X.astype(np.float32)
+        rc_a, want = _run(lib.locomp_amd_dequant_matvec_int4, X, W, S, M, N, K, G, _lib.F32)
+        rc_b, got = _run(lib.locomp_amd_dequant_matvec_int4_noalloc, X, W, S, M, N, K, G, _lib.F32)
         assert rc_a == 0 and rc_b == 0, (rc_a, rc_b)
         assert not np.isnan(got).any()
         assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
