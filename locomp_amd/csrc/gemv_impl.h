@@ -266,29 +266,35 @@ static bool gemv_tile_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, 
 
 // 16 < M <= 64 on the activation-in-LDS ring: K % 256, G % 32, fp16
 // activations; T = 1..4 tiles so the grid is at most one workgroup per CU,
-// while the workgroup's scale rows fit 16 KB and the array is whole dwords.
-static int gemv_tile_xl_count(int wbits, int64_t N, int64_t K, int64_t G, int scale_bytes) {
+// while the workgroup's scale rows fit the LDS the ring leaves (which
+// depends on the activation tile count mt) and the array is whole dwords.
+static int gemv_tile_xl_count(int wbits, int64_t N, int64_t K, int64_t G, int scale_bytes,
+                              int mt) {
   int tiles = 4;
   for (int t = 1; t <= 4; ++t)
     if ((N + 16 * t - 1) / (16 * t) <= 256) { tiles = t; break; }
   // int4 rows are 128 bytes per chunk: whole 1 KB DMA instructions need T even
   if (wbits == 4 && (tiles & 1)) ++tiles;
-  while (tiles > 0 && 16 * tiles * (K / G) * scale_bytes > xl_scale_bytes(wbits, tiles))
+  while (tiles > 0 && 16 * tiles * (K / G) * scale_bytes > xl_scale_bytes(wbits, tiles, mt))
     tiles -= wbits == 4 ? 2 : 1;
   return tiles;
 }
+// activation tiles: 1 up to 16 rows (int8 only), 2 up to 32, else 4
+static inline int xl_mtiles(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 static bool gemv_tile_xl_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G, int scale_bytes) {
-  return M > 16 && M <= 64 && K % kXChunkK == 0 && K < (int64_t(1) << 22) && G % 32 == 0 &&
-         (N * (K / G) * scale_bytes) % 4 == 0 && gemv_tile_xl_count(wbits, N, K, G, scale_bytes) > 0;
+  return (M > 16 || wbits == 8) && M >= 1 && M <= 64 && K % kXChunkK == 0 &&
+         K < (int64_t(1) << 22) && G % 32 == 0 &&
+         (N * (K / G) * scale_bytes) % 4 == 0 &&
+         gemv_tile_xl_count(wbits, N, K, G, scale_bytes, xl_mtiles(M)) > 0;
 }
-template <int WBITS, int SD, int OD, bool EPI = false>
-static int launch_gemv_tile_xl(const void* X, const void* W, const void* S, void* O, int64_t M,
-                               int64_t N, int64_t K, int64_t G, hipStream_t st) {
-  const int tiles = gemv_tile_xl_count(WBITS, N, K, G, SD == LQ_F32 ? 4 : 2);
+template <int WBITS, int SD, int OD, bool EPI, int MT>
+static void launch_gemv_tile_xl_mt(const void* X, const void* W, const void* S, void* O, int64_t M,
+                                   int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int tiles = gemv_tile_xl_count(WBITS, N, K, G, SD == LQ_F32 ? 4 : 2, MT);
   const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
 #define LQ_TX(T_)                                                                              \
-  hipLaunchKernelGGL((gemv_tile_xl_kernel<WBITS, T_, SD, OD, EPI>), dim3(blocks), dim3(512), 0, st, \
-                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,     \
+  hipLaunchKernelGGL((gemv_tile_xl_kernel<WBITS, T_, SD, OD, EPI, MT>), dim3(blocks), dim3(512), 0, \
+                     st, static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,  \
                      int(M), int(N), int(K), int(K / G), int(G))
   if constexpr (WBITS == 8) {
     switch (tiles) {
@@ -302,6 +308,19 @@ static int launch_gemv_tile_xl(const void* X, const void* W, const void* S, void
     else LQ_TX(4);
   }
 #undef LQ_TX
+}
+template <int WBITS, int SD, int OD, bool EPI = false>
+static int launch_gemv_tile_xl(const void* X, const void* W, const void* S, void* O, int64_t M,
+                               int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  const int mt = xl_mtiles(M);
+  if constexpr (WBITS == 8) {
+    if (mt == 1) {
+      launch_gemv_tile_xl_mt<WBITS, SD, OD, EPI, 1>(X, W, S, O, M, N, K, G, st);
+      return check_launch();
+    }
+  }
+  if (mt <= 2) launch_gemv_tile_xl_mt<WBITS, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
+  else launch_gemv_tile_xl_mt<WBITS, SD, OD, EPI, 4>(X, W, S, O, M, N, K, G, st);
   return check_launch();
 }
 
@@ -335,6 +354,14 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
   // the LDS-ring tile kernel also serves bf16 scales / outputs (not mixed
   // with fp32, to bound the instantiations)
   constexpr bool kTileDt = !(SD == LQ_F32 && OD == LQ_BF16) && !(SD == LQ_BF16 && OD == LQ_F32);
+  if constexpr (kTileDt && WBITS == 8) {
+    // int8, 8 < M <= 16, scale groups of whole 256-k chunks (per channel):
+    // the activation-in-LDS kernel with one activation tile (its raw sums
+    // span a group; 4096 x 4096 per channel M = 16: 8.9 against 10.7 us).
+    // Smaller M or groups take the ring tile kernel below.
+    if (M > 8 && G % kXChunkK == 0 && gemv_tile_xl_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
+      return launch_gemv_tile_xl<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
+  }
   if constexpr (kTileDt) {
     // int4 M = 1 keeps the segment / row kernels up to K = 8192 (faster there);
     // longer rows stream better through the LDS ring.  int4 M = 2 also takes

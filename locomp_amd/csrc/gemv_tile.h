@@ -345,17 +345,19 @@ constexpr int kXChunkK = 256;
 constexpr int kXSlots = 3;
 // LDS of the ring (also the cross-wave sum) and of the scale rows: whatever
 // the ring leaves of 160 KB, at most kTScaleLds.
-constexpr int xl_ring_bytes(int wbits, int tiles) {
-  const int slot = 16 * tiles * kXChunkK * wbits / 8 + 64 * kXChunkK * 2;
-  return kXSlots * slot > 8 * 4 * tiles * 1024 ? kXSlots * slot : 8 * 4 * tiles * 1024;
+constexpr int xl_ring_bytes(int wbits, int tiles, int mtiles) {
+  const int slot = 16 * tiles * kXChunkK * wbits / 8 + 16 * mtiles * kXChunkK * 2;
+  const int red = 8 * mtiles * tiles * 1024;
+  return kXSlots * slot > red ? kXSlots * slot : red;
 }
-constexpr int xl_scale_bytes(int wbits, int tiles) {
-  const int left = 160 * 1024 - xl_ring_bytes(wbits, tiles);
+constexpr int xl_scale_bytes(int wbits, int tiles, int mtiles) {
+  const int left = 160 * 1024 - xl_ring_bytes(wbits, tiles, mtiles);
   return (left > kTScaleLds ? kTScaleLds : left) & ~1023;
 }
 
 // EPI: gate/up rows interleaved; store silu(gate) * up to O [M, N / 2].
-template <int WBITS, int TILES, int SD, int OD, bool EPI = false>
+// MT: 16-row activation tiles (2 for M <= 32, else 4).
+template <int WBITS, int TILES, int SD, int OD, bool EPI = false, int MT = 4>
 __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
   constexpr int kRowB = kXChunkK * WBITS / 8;             // weight bytes per row per chunk
   constexpr int kPos = kRowB / 16;                        // 16-byte positions per weight row
   constexpr int kWBytes = kRows * kRowB;
-  constexpr int kXBytes = 64 * kXChunkK * 2;              // 64 activation rows, fp16
+  constexpr int kXBytes = 16 * MT * kXChunkK * 2;         // 16 MT activation rows, fp16
   constexpr int kSlotB = kWBytes + kXBytes;
   constexpr int kSSize = SD == LQ_F32 ? 4 : 2;
   constexpr int kWInstr = kWBytes / 1024;
@@ -374,9 +376,9 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
   constexpr int kPerWaveMax = (kInstr + 7) / 8;
   static_assert(kWBytes % 1024 == 0, "whole weight DMA instructions");
   // the cross-wave sum reuses the ring (sized to hold it)
-  constexpr int kRingB = xl_ring_bytes(WBITS, TILES);
+  constexpr int kRingB = xl_ring_bytes(WBITS, TILES, MT);
   static_assert(kRingB >= kXSlots * kSlotB, "ring holds the slots");
-  constexpr int kSclB = xl_scale_bytes(WBITS, TILES);
+  constexpr int kSclB = xl_scale_bytes(WBITS, TILES, MT);
   static_assert(kRingB + kSclB <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(16))) uint8_t ring[kRingB];
   __shared__ __attribute__((aligned(16))) uint8_t sl[kSclB];
@@ -452,20 +454,20 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
   }
 
   const uint32_t magic = opaque_u32(0x64006400u);
-  float4_t acc[4][TILES];
+  float4_t acc[MT][TILES];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int t = 0; t < TILES; ++t) acc[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   // int8: raw sums over the chunks of one scale group, scaled into acc when
   // the group changes (per-channel scales: once, after the last chunk).
-  float4_t raw[4][TILES];
+  float4_t raw[MT][TILES];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int t = 0; t < TILES; ++t) raw[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
-  auto add_scaled = [&](const float4_t (&part)[4][TILES], int g) {
+  auto add_scaled = [&](const float4_t (&part)[MT][TILES], int g) {
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
       const uint8_t* ps = sl + (size_t(t * 16 + r16) * num_scales + g) * kSSize;
@@ -474,7 +476,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
       else if constexpr (SD == LQ_F16) sc = float(*reinterpret_cast<const half_t*>(ps));
       else sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
         acc[mt][t] += part[mt][t] * sc;
         // keep the MFMA-result read in this block (see gemv_tile_kernel)
         __asm__ volatile("" : "+v"(acc[mt][t]));
@@ -507,7 +509,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
         bw[t] = h8{lo[0][0], lo[0][1], lo[1][0], lo[1][1], hi[0][0], hi[0][1], hi[1][0], hi[1][1]};
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
         const int row = mt * 16 + r16;
         const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(
             xl + row * (kXChunkK * 2) + (((4 * wave + q4) ^ (row & 15)) << 4));
@@ -520,14 +522,14 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
         left = cpg;
         add_scaled(raw, div_rcp(pc * kXChunkK + wave * 32, group, rgroup));
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int t = 0; t < TILES; ++t) raw[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
       }
     } else {
       // one 16x16x32 block: the lane's 8 k are wave * 32 + q4 * 8 .., i.e.
       // dword q4 of weight chunk `wave` and activation bytes 64 w + 16 q4
-      float4_t part[4][TILES];
+      float4_t part[MT][TILES];
       op_t bw[TILES];
 #pragma unroll
       for (int t = 0; t < TILES; ++t) {
@@ -538,7 +540,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
       }
       const op_t nb = Mf::neg_bias();
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
         const int row = mt * 16 + r16;
         const int chunk = wave * 4 + q4;
         const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(
@@ -565,15 +567,15 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
 
   float4_t* red = reinterpret_cast<float4_t*>(ring);
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) red[((wave * 4 + mt) * TILES + t) * 64 + lane] = acc[mt][t];
+    for (int t = 0; t < TILES; ++t) red[((wave * MT + mt) * TILES + t) * 64 + lane] = acc[mt][t];
   __syncthreads();
-  for (int pidx = wave; pidx < 4 * TILES; pidx += 8) {
+  for (int pidx = wave; pidx < MT * TILES; pidx += 8) {
     const int mt = pidx / TILES, t = pidx % TILES;
     float4_t v = red[(mt * TILES + t) * 64 + lane];
 #pragma unroll
-    for (int w2 = 1; w2 < 8; ++w2) v += red[((w2 * 4 + mt) * TILES + t) * 64 + lane];
+    for (int w2 = 1; w2 < 8; ++w2) v += red[((w2 * MT + mt) * TILES + t) * 64 + lane];
     const int n = n0 + t * 16 + r16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {

@@ -195,7 +195,8 @@ def test_matvec_lds_ring_shapes(wbits, M, N, K, G):
 @pytest.mark.parametrize("M,N,K,G", [
     (17, 64, 1024, 64), (33, 300, 2048, 16), (64, 1000, 4096, 4096), (48, 4100, 1536, 512),
     (16, 1000, 4096, 4096), (3, 77, 1024, 1024), (32, 11008, 4096, 128), (64, 9000, 768, 32),
-    (40, 500, 1536, 384), (24, 333, 3072, 768), (64, 14336, 4096, 4096)])
+    (40, 500, 1536, 384), (24, 333, 3072, 768), (64, 14336, 4096, 4096), (12, 777, 2048, 512),
+    (9, 4100, 1024, 1024)])
 def test_matvec_many_rows_and_per_channel(wbits, M, N, K, G):
     """Decode/verify sizes up to M = 64 and per-channel / large groups
     (one or few scales per row, whose scale rows are not 16-byte multiples).
