@@ -101,12 +101,11 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
       if (r * NSEG + c < kEarly) wload(r, c);
   __builtin_amdgcn_sched_barrier(0);
 
-  // 4. activation operands and bias accumulators, built once per workgroup
-  // in LDS: every thread converts M_ * NSEG of the 16-byte chunks (chunk
-  // (m, c, lane, e) -> slot), then waves 0.. compute -bias for one (m, c)
-  // each with 4 MFMAs, then every wave reads its operands back.
+  // 4. activation operands, built once per workgroup in LDS: every thread
+  // converts M_ * NSEG of the 16-byte chunks (chunk (m, c, lane, e) -> slot);
+  // then the bias chains, the remaining weight loads, and every wave reads
+  // its operands back.
   __shared__ u32x4_t xs_l[M_ * NSEG * NP * 256];
-  __shared__ float4_t nc_l[M_ * NSEG * 64];
   const half2_t sixteenth = {half_t(0.0625f), half_t(0.0625f)};
   {
     const int t = threadIdx.x;
@@ -133,33 +132,45 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
       }
   }
   __syncthreads();
-  {
-    for (int mc = wave; mc < M_ * NSEG; mc += 4) {
-      float4_t cr = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (kH) {
-        const half2_t b1032 = {half_t(1032.f), half_t(1032.f)};
-        const half2_t b1152 = {half_t(1152.f), half_t(1152.f)};
-        u32x4_t bias_w;
-        bias_w.x = as_u32(b1032); bias_w.y = as_u32(b1152); bias_w.z = as_u32(b1032); bias_w.w = as_u32(b1152);
-        const h8 bias_op = __builtin_bit_cast(h8, bias_w);
+  // -bias * x per (row, segment), 4 MFMAs (x NP parts) each: fp16 activations
+  // form them in every wave (no second barrier before the remaining weight
+  // loads); bf16 / fp32 ones, whose chains are longer, once per workgroup in
+  // LDS (waves 0.. one (m, c) each).
+  constexpr bool kOwnBias = kH;
+  auto bias_chain = [&](const u32x4_t* xe /* [NP][4] */) {
+    float4_t cr = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kH) {
+      const half2_t b1032 = {half_t(1032.f), half_t(1032.f)};
+      const half2_t b1152 = {half_t(1152.f), half_t(1152.f)};
+      u32x4_t bias_w;
+      bias_w.x = as_u32(b1032); bias_w.y = as_u32(b1152); bias_w.z = as_u32(b1032); bias_w.w = as_u32(b1152);
+      const h8 bias_op = __builtin_bit_cast(h8, bias_w);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, xe[e]), bias_op, cr, 0, 0, 0);
+    } else {
+      const u32x4_t b136 = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};   // 128 + 8
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              __builtin_bit_cast(h8, xs_l[mc * 256 + lane * 4 + e]), bias_op, cr, 0, 0, 0);
-      } else {
-        const u32x4_t b136 = {0x43084308u, 0x43084308u, 0x43084308u, 0x43084308u};   // 128 + 8
-#pragma unroll
-        for (int p = 0; p < NP; ++p)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            cr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf8_t, xs_l[(mc * NP + p) * 256 + lane * 4 + e]),
-                __builtin_bit_cast(bf8_t, b136), cr, 0, 0, 0);
-      }
-      nc_l[mc * 64 + lane] = -cr;
+          cr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8_t, xe[p * 4 + e]),
+                                                       __builtin_bit_cast(bf8_t, b136), cr, 0, 0, 0);
     }
+    return -cr;
+  };
+  __shared__ float4_t nc_l[kOwnBias ? 1 : M_ * NSEG * 64];
+  if constexpr (!kOwnBias) {
+    for (int mc = wave; mc < M_ * NSEG; mc += 4) {
+      u32x4_t xe[NP * 4];
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xe[p * 4 + e] = xs_l[(mc * NP + p) * 256 + lane * 4 + e];
+      nc_l[mc * 64 + lane] = bias_chain(xe);
+    }
+    __syncthreads();
   }
-  __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int r = 0; r < RW; ++r)
@@ -177,7 +188,8 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
       for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int e = 0; e < 4; ++e) xv[m][c][p][e] = xs_l[((m * NSEG + c) * NP + p) * 256 + lane * 4 + e];
-      negcorr[m][c] = nc_l[(m * NSEG + c) * 64 + lane];
+      if constexpr (kOwnBias) negcorr[m][c] = bias_chain(&xv[m][c][0][0]);
+      else negcorr[m][c] = nc_l[(m * NSEG + c) * 64 + lane];
     }
 
   // 5. rows: decode (5 ops / 8 weights) + MFMA, chains start at -bias
