@@ -33,6 +33,9 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   constexpr bool kH = XD == LQ_F16;
   constexpr int NP = XD == LQ_F32 ? 3 : 1;     // bf16 parts per activation
   constexpr int kXB = XD == LQ_F32 ? 4 : 2;    // activation element bytes
+  // load the output pointer now (else its kernel-argument load sits between
+  // the final reduction and the store)
+  __asm__ volatile("" ::"s"(reinterpret_cast<uint64_t>(O)));
   const int sd = SD == kRT ? sd_rt : SD;
   const int ssz = sd == LQ_F32 ? 4 : 2;
   const float rgroup = 1.0f / float(group);    // for div_rcp (K <= 16384 here)
@@ -271,8 +274,16 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
         v[i] = keep + __shfl_xor(send, width, 64);
       }
     }
+    // the remaining full sum: LDS shuffles across the 16-lane rows, then an
+    // in-row prefix sum by DPP row shifts (VALU latency instead of one LDS
+    // round trip per step), which leaves the sum of each span of 2 width
+    // lanes in its last lane
 #pragma unroll
-    for (; width > 0; width >>= 1) v[0] += __shfl_xor(v[0], width, 64);
+    for (; width >= 16; width >>= 1) v[0] += __shfl_xor(v[0], width, 64);
+    if (width >= 1) v[0] += dpp_row_shr<1>(v[0]);
+    if (width >= 2) v[0] += dpp_row_shr<2>(v[0]);
+    if (width >= 4) v[0] += dpp_row_shr<4>(v[0]);
+    if (width >= 8) v[0] += dpp_row_shr<8>(v[0]);
     int row = 0;
     {
       int w2 = 32;
@@ -280,7 +291,8 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
       for (int c2 = RW; c2 > 1; c2 >>= 1, w2 >>= 1) row = row * 2 + ((lane & w2) ? 1 : 0);
     }
     const int lowmask = (64 / RW) - 1;
-    if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_out<OD>(O, size_t(m) * N + n0 + row, v[0], od_rt);
+    if ((lane & lowmask) == lowmask && m < M && n0 + row < N)
+      store_out<OD>(O, size_t(m) * N + n0 + row, v[0], od_rt);
   }
 }
 

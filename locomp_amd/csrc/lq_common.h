@@ -180,6 +180,14 @@ __device__ __forceinline__ int div_rcp(int a, int d, float rd) {
   return q;
 }
 
+// v of the lane N below in the same 16-lane row (DPP row_shr:N), 0 for the
+// row's first N lanes.
+template <int N>
+__device__ __forceinline__ float dpp_row_shr(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x110 + N, 0xF, 0xF, true));
+}
+
 // A value the optimiser cannot constant-fold (held in a VGPR).
 __device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
   __asm__ volatile("" : "+v"(v));
