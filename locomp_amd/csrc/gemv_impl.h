@@ -365,9 +365,10 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
   if constexpr (kTileDt) {
     // int4 M = 1 keeps the segment / row kernels up to K = 8192 (faster there);
     // longer rows stream better through the LDS ring.  int4 M = 2 also takes
-    // the segment kernel for K >= 4096 and N <= 8192 (4096 x 4096: 4.9 against
-    // 6.1 us; at N = 11008 or K = 2048 the ring wins).
-    const bool seg2 = WBITS == 4 && M == 2 && K >= 4096 && N <= 8192 && gemv_seg_ok(WBITS, M, N, K, G);
+    // the segment kernel for K >= 4096 (4096 x 4096: 4.7 against 6.0 us,
+    // 11008 x 4096: 8.1 against 8.8; at K = 2048, and at M = 3, 4 with
+    // N >= 11008, the ring wins).
+    const bool seg2 = WBITS == 4 && M == 2 && K >= 4096 && gemv_seg_ok(WBITS, M, N, K, G);
     if (!seg2 && (M >= 2 || WBITS == 8 || K > 8192) && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
