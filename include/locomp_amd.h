@@ -17,10 +17,12 @@
  * rows M, element dtypes, a HIP stream).
  *
  * Conventions
- *   - All pointers are device pointers.  The library allocates only a
- *     grow-only fp32 workspace per (device, stream), on the first prefill
- *     that splits K and on the first SiLU * mul call without a fused kernel;
- *     it is held until the process ends or locomp_amd_release_workspaces.
+ *   - All pointers are device pointers.  The library allocates only
+ *     grow-only workspaces per (device, stream): on the first prefill that
+ *     splits K, on the first SiLU * mul call without a fused kernel, and on
+ *     the first fp32-activation decode call at M <= 4 (its bf16 part rows,
+ *     24 K bytes); they are held until the process ends or
+ *     locomp_amd_release_workspaces.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
  *     is asynchronous: the caller synchronises.
  *   - Return value: 0 on success; a negative LQ_ERR_* for invalid arguments
@@ -122,8 +124,9 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * M <= 64 runs the decode (skinny) kernel, larger M the prefill MFMA GEMM.
  * Activations may be fp16, bf16 or fp32 (the reference's dtype): fp16 and
  * bf16 run on fp16 / bf16 matrix cores at every M; fp32 at M <= 4 runs on
- * bf16 matrix cores as three exact bf16 parts; other fp32 shapes take a
- * generic kernel.  The fast kernels need X and W 16-byte aligned and the
+ * bf16 matrix cores as three exact bf16 parts (split once per call into a
+ * workspace, or inside the kernel on a capturing stream that has none yet);
+ * other fp32 shapes take a generic kernel.  The fast kernels need X and W 16-byte aligned and the
  * scales 4-byte aligned (otherwise a generic kernel runs).
  * A prefill GEMM with fewer output tiles than CUs splits K and keeps an fp32
  * workspace per (device, stream), allocated on first use and held until the
@@ -139,9 +142,10 @@ int locomp_amd_dequant_matvec_int4(const void* X, const void* W,
 /* As locomp_amd_dequant_matvec_int4, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference.  Same kernels and
- * results; the split-K prefill's fp32 partials go to a fixed 32 MiB array in
- * the library's device memory (one per GPU, held until the process ends)
- * instead of the per-stream workspace, and the call allocates nothing.  A
+ * results; the split-K prefill's fp32 partials (and the bf16 part rows of
+ * fp32 activations at M <= 4) go to a fixed 32 MiB array in the library's
+ * device memory (one per GPU, held until the process ends) instead of the
+ * per-stream workspaces, and the call allocates nothing.  A
  * call whose split-K plan needs more (M x N x 4 bytes x splits: e.g. beyond
  * M = 512 at N = 4096) returns LQ_ERR_SCRATCH and launches nothing.  All calls
  * on one GPU share its array: calls that overlap in time on one GPU (several
