@@ -369,7 +369,11 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
     // 11008 x 4096: 8.1 against 8.8; at K = 2048, and at M = 3, 4 with
     // N >= 11008, the ring wins).
     const bool seg2 = WBITS == 4 && M == 2 && K >= 4096 && gemv_seg_ok(WBITS, M, N, K, G);
-    if (!seg2 && (M >= 2 || WBITS == 8 || K > 8192) && gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
+    // int4 M = 1 with K > 8192: the segment kernel up to N = 8192 (4096 x
+    // 11008: 9.6 against 11.4 us), the ring beyond (11008 x 11008: 18 against 22)
+    const bool seg1 = WBITS == 4 && M == 1 && K > 8192 && N <= 8192 && gemv_seg_ok(WBITS, M, N, K, G);
+    if (!seg2 && !seg1 && (M >= 2 || WBITS == 8 || K > 8192) &&
+        gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }
   if constexpr (kTileDt) {

@@ -137,8 +137,9 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   __syncthreads();
   // -bias * x per (row, segment), 4 MFMAs (x NP parts) each: fp16 activations
   // form them in every wave (no second barrier before the remaining weight
-  // loads); bf16 / fp32 ones, whose chains are longer, once per workgroup in
-  // LDS (waves 0.. one (m, c) each).
+  // loads; measured faster also at 8 segments of one row per wave, where the
+  // chains equal the row's own MFMAs); bf16 / fp32 ones, whose chains are
+  // longer, once per workgroup in LDS (waves 0.. one (m, c) each).
   constexpr bool kOwnBias = kH;
   auto bias_chain = [&](const u32x4_t* xe /* [NP][4] */) {
     float4_t cr = {0.f, 0.f, 0.f, 0.f};
