@@ -25,8 +25,11 @@ __global__ __launch_bounds__(256, 3) void gemv_rows_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
   typedef typename Elem<SD>::T stype;
+  // load the output pointer now (else its kernel-argument load sits between
+  // the final reduction and the store)
+  __asm__ volatile("" ::"s"(reinterpret_cast<uint64_t>(O)));
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (SGPR)
   const int n0 = (blockIdx.x * 4 + wave) * RW;
   const int half_k = K >> 1;
 
@@ -144,8 +147,15 @@ __global__ __launch_bounds__(256, 3) void gemv_rows_kernel(
         v[i] = keep + __shfl_xor(send, width, 64);
       }
     }
+    // the remaining full sum: LDS shuffles across the 16-lane rows, then an
+    // in-row prefix sum by DPP row shifts, which leaves the sum of each span
+    // of 2 width lanes in its last lane
 #pragma unroll
-    for (; width > 0; width >>= 1) v[0] += __shfl_xor(v[0], width, 64);
+    for (; width >= 16; width >>= 1) v[0] += __shfl_xor(v[0], width, 64);
+    if (width >= 1) v[0] += dpp_row_shr<1>(v[0]);
+    if (width >= 2) v[0] += dpp_row_shr<2>(v[0]);
+    if (width >= 4) v[0] += dpp_row_shr<4>(v[0]);
+    if (width >= 8) v[0] += dpp_row_shr<8>(v[0]);
     // lane bits 5..(6 - log2 RW) name the row
     int row = 0;
     {
@@ -158,12 +168,13 @@ __global__ __launch_bounds__(256, 3) void gemv_rows_kernel(
       static_assert(RW % 2 == 0, "gate / up pairs within one wave");
       // row r and r ^ 1 sit in lanes that differ in bit log2(64 / RW)
       const float other = __shfl_xor(v[0], 64 / RW, 64);
-      if ((lane & lowmask) == 0 && (row & 1) == 0 && m < M && n0 + row + 1 < N) {
+      if ((lane & lowmask) == lowmask && (row & 1) == 0 && m < M && n0 + row + 1 < N) {
         const float g = v[0];
         store_f32<OD>(O, size_t(m) * (N >> 1) + ((n0 + row) >> 1), g / (1.0f + expf(-g)) * other);
       }
     } else {
-      if ((lane & lowmask) == 0 && m < M && n0 + row < N) store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+      if ((lane & lowmask) == lowmask && m < M && n0 + row < N)
+        store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
     }
   }
 }
