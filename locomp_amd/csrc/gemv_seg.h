@@ -86,11 +86,12 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
     }
   __builtin_amdgcn_sched_barrier(0);
   // 3. weights: the first kEarly chunks now, the rest after the operand
-  // barriers below.  A wave reaches a barrier only once it has issued every
+  // barrier below.  A wave reaches a barrier only once it has issued every
   // load before it, and issue stalls while the CU's memory queue is full, so
   // issuing all weights here made each workgroup wait for its slowest issuer
-  // (operands ready 1.1-4.0 us after the start; 0.8-1.8 us this way).
-  constexpr int kEarly = 2;
+  // (with two barriers; with one, 4 of 8 early chunks measured best at M = 1,
+  // 5.86 against 6.00 us, while M = 2 keeps 2: 8.0 against 8.7 us).
+  constexpr int kEarly = M_ == 1 ? 4 : 2;
   u32x4_t wv[RW][NSEG];
   auto wload = [&](int r, int c) {
     wv[r][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
@@ -136,11 +137,12 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
   }
   __syncthreads();
   // -bias * x per (row, segment), 4 MFMAs (x NP parts) each: fp16 activations
-  // form them in every wave (no second barrier before the remaining weight
-  // loads; measured faster also at 8 segments of one row per wave, where the
-  // chains equal the row's own MFMAs); bf16 / fp32 ones, whose chains are
-  // longer, once per workgroup in LDS (waves 0.. one (m, c) each).
-  constexpr bool kOwnBias = kH;
+  // at M = 1 form them in every wave (no second barrier before the remaining
+  // weight loads; measured faster also at 8 segments of one row per wave,
+  // where the chains equal the row's own MFMAs); M = 2 (twice the chains:
+  // 8.7 against 7.8 us at 11008 x 4096) and bf16 / fp32 activations, whose
+  // chains are longer, once per workgroup in LDS (waves 0.. one (m, c) each).
+  constexpr bool kOwnBias = kH && M_ == 1;
   auto bias_chain = [&](const u32x4_t* xe /* [NP][4] */) {
     float4_t cr = {0.f, 0.f, 0.f, 0.f};
     if constexpr (kH) {
