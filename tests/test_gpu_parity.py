@@ -170,7 +170,9 @@ def _close(got, want, fp32=False):
 @pytest.mark.parametrize("M,N,K,G", [
     (1, 64, 256, 32), (4, 100, 512, 128), (16, 48, 1024, 1024), (3, 17, 96, 32),
     (1, 192, 576, 32), (1, 576, 1536, 32), (33, 40, 256, 64), (64, 80, 512, 512),
-    (2, 7, 40, 8), (5, 9, 16, 16)])
+    (2, 7, 40, 8), (5, 9, 16, 16),
+    (2, 3072, 576, 32),    # row kernel, one row per wave, two activation rows
+    (1, 3100, 1024, 32)])  # row kernel, four rows per wave (N > 3072), ragged
 def test_matvec_fp16_small(policy, wbits, M, N, K, G):
     X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=M * 1000 + N)
     got = _matvec(wbits, X, W, S, N, K, G, "f16")
@@ -239,6 +241,7 @@ def test_int8_prefill_large():
     (4, 257, 14336, 128),     # 7 segments -> 8
     (1, 100, 3200, 640),
     (2, 4096, 4096, 128),     # M = 2 on the segment kernel (whole segments)
+    (2, 11008, 4096, 128),    # M = 2 on the segment kernel at cfg 3's N
     (2, 1000, 5120, 128),     # M = 2, 2.5 segments -> 4
 ])
 def test_matvec_int4_partial_segment(M, N, K, G):
