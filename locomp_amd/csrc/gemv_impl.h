@@ -107,11 +107,11 @@ static int launch_gemv_lds_p(const void* X, const void* W, const void* S, void* 
 }
 
 
-template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false>
+template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3>
 static int launch_gemv_rows_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                               int64_t N, int64_t K, int64_t G, hipStream_t st) {
   const unsigned blocks = unsigned((N + 4 * RW - 1) / (4 * RW));
-  hipLaunchKernelGGL((gemv_rows_kernel<M_, NSEG, RW, SD, OD, EPI>), dim3(blocks), dim3(256), 0, st,
+  hipLaunchKernelGGL((gemv_rows_kernel<M_, NSEG, RW, SD, OD, EPI, OCC>), dim3(blocks), dim3(256), 0, st,
                      static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
                      int(N), int(K), int(K / G), int(G));
   return check_launch();
@@ -132,7 +132,8 @@ static int launch_gemv_rows_m(const void* X, const void* W, const void* S, void*
   if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
   if (nseg <= 2) return launch_gemv_rows_t<M_, 2, 4, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
   if (nseg <= 4) return launch_gemv_rows_t<M_, 4, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
-  return launch_gemv_rows_t<M_, 8, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+  // 8 segments (K <= 16384, M = 1): 237 VGPRs, sized for 2 workgroups per CU
+  return launch_gemv_rows_t<M_, 8, 2, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
 }
 
 template <int M_, int NSEG, int RW, int SD, int OD>
@@ -345,7 +346,7 @@ static bool gemv_diag_ok(int wbits, int64_t M, int64_t K, int64_t G) {
 // K <= 16384.
 static bool gemv_rows_ok(int wbits, int64_t M, int64_t K, int64_t G) {
   return wbits == 4 && M <= 2 && K % 32 == 0 && G % 32 == 0 && K >= 32 &&
-         K <= (M == 1 ? 8192 : 2048);
+         K <= (M == 1 ? 16384 : 2048);
 }
 
 template <int WBITS, int MT, int SD, int OD>
@@ -380,7 +381,11 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
     // int4 M = 1 with K > 8192: the segment kernel up to N = 8192 (4096 x
     // 11008: 9.6 against 11.4 us), the ring beyond (11008 x 11008: 18 against 22)
     const bool seg1 = WBITS == 4 && M == 1 && K > 8192 && N <= 8192 && gemv_seg_ok(WBITS, M, N, K, G);
-    if (!seg2 && !seg1 && (M >= 2 || WBITS == 8 || K > 8192) &&
+    // int4 M = 1 with K > 8192 and groups the segment kernel cannot take
+    // (G % 128 != 0): the row kernel at 8 segments (G = 32: 4096 x 11008 10.0
+    // against 13.0 us, 11008 x 11008 21.7 against 31.3)
+    const bool rows1 = WBITS == 4 && M == 1 && K > 8192 && G % 128 != 0 && gemv_rows_ok(WBITS, M, K, G);
+    if (!seg2 && !seg1 && !rows1 && (M >= 2 || WBITS == 8 || K > 8192) &&
         gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }

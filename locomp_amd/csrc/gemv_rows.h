@@ -20,8 +20,9 @@ namespace lq {
 // EPI: the weight rows are gate / up interleaved (row 2i = gate_i, 2i + 1 =
 // up_i) and the kernel stores silu(gate_i) * up_i to O [M, N / 2] instead of
 // the N dot products (examples/54_smollm2_inference.py:113-120, 545-548).
-template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false>
-__global__ __launch_bounds__(256, 3) void gemv_rows_kernel(
+// OCC: workgroups per CU the register budget is sized for (2 for 8 segments).
+template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3>
+__global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
   typedef typename Elem<SD>::T stype;

@@ -242,6 +242,8 @@ def test_int8_prefill_large():
     (1, 100, 3200, 640),
     (2, 4096, 4096, 128),     # M = 2 on the segment kernel (whole segments)
     (2, 11008, 4096, 128),    # M = 2 on the segment kernel at cfg 3's N
+    (1, 4096, 11008, 32),     # G % 128 != 0: the row kernel at 8 segments
+    (1, 300, 14336, 64),
     (2, 1000, 5120, 128),     # M = 2, 2.5 segments -> 4
 ])
 def test_matvec_int4_partial_segment(M, N, K, G):
@@ -510,6 +512,7 @@ def _silu_mul_oracle(X, Wg, Sg, Wu, Su, G):
     (300, 1100, 512, 64, "f16"),    # prefill GEMM epilogue, ragged tiles
     (1100, 2048, 1024, 128, "f16"), # 256-row tiles
     (40, 300, 576, 32, "f16"),      # no fused kernel: staged fp32 matvec + pairwise epilogue
+    (1, 700, 11008, 32, "f16"),     # row kernel at 8 segments with the epilogue
     (8, 100, 576, 64, "f16"),
 ])
 def test_matvec_int4_silu_mul(policy, M, I, K, G, xd):
