@@ -130,7 +130,8 @@ static int launch_gemv_rows_m(const void* X, const void* W, const void* S, void*
     return launch_gemv_rows_t<M_, 2, kSmallRW, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
   }
   if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
-  if (nseg <= 2) return launch_gemv_rows_t<M_, 2, 4, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+  // (two activation rows x 2 segments: 210 VGPRs, sized for 2 workgroups per CU)
+  if (nseg <= 2) return launch_gemv_rows_t<M_, 2, 4, SD, OD, EPI, M_ == 2 ? 2 : 3>(X, W, S, O, M, N, K, G, st);
   if (nseg <= 4) return launch_gemv_rows_t<M_, 4, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
   // 8 segments (K <= 16384, M = 1): 237 VGPRs, sized for 2 workgroups per CU
   return launch_gemv_rows_t<M_, 8, 2, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
@@ -346,7 +347,7 @@ static bool gemv_diag_ok(int wbits, int64_t M, int64_t K, int64_t G) {
 // K <= 16384.
 static bool gemv_rows_ok(int wbits, int64_t M, int64_t K, int64_t G) {
   return wbits == 4 && M <= 2 && K % 32 == 0 && G % 32 == 0 && K >= 32 &&
-         K <= (M == 1 ? 16384 : 2048);
+         K <= (M == 1 ? 16384 : 4096);
 }
 
 template <int WBITS, int MT, int SD, int OD>
@@ -385,7 +386,10 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
     // (G % 128 != 0): the row kernel at 8 segments (G = 32: 4096 x 11008 10.0
     // against 13.0 us, 11008 x 11008 21.7 against 31.3)
     const bool rows1 = WBITS == 4 && M == 1 && K > 8192 && G % 128 != 0 && gemv_rows_ok(WBITS, M, K, G);
-    if (!seg2 && !seg1 && !rows1 && (M >= 2 || WBITS == 8 || K > 8192) &&
+    // int4 M = 2 with G % 128 != 0 and K <= 4096: the row kernel (G = 32:
+    // 11008 x 4096 9.0 against 13.0 us, 4096 x 4096 5.0 against 7.1)
+    const bool rows2 = WBITS == 4 && M == 2 && G % 128 != 0 && gemv_rows_ok(WBITS, M, K, G);
+    if (!seg2 && !seg1 && !rows1 && !rows2 && (M >= 2 || WBITS == 8 || K > 8192) &&
         gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }

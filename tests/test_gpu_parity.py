@@ -244,6 +244,8 @@ def test_int8_prefill_large():
     (2, 11008, 4096, 128),    # M = 2 on the segment kernel at cfg 3's N
     (1, 4096, 11008, 32),     # G % 128 != 0: the row kernel at 8 segments
     (1, 300, 14336, 64),
+    (2, 11008, 4096, 32),     # M = 2, G % 128 != 0: the row kernel, 2 segments
+    (2, 333, 3200, 64),       # ragged, partial second segment
     (2, 1000, 5120, 128),     # M = 2, 2.5 segments -> 4
 ])
 def test_matvec_int4_partial_segment(M, N, K, G):
