@@ -254,6 +254,23 @@ def test_matvec_int4_partial_segment(M, N, K, G):
     _close(got, _oracle(4, X, W, S, G))
 
 
+# Both sides of every int4 M <= 2 routing limit (the kernel choice changes at
+# each): M = 1 K = 8192 / 8448 (row kernel at 4 / 8 segments), K = 16384 /
+# 16512 (row kernel's last K, then the ring tile kernel), N = 8192 / 8193 at
+# K > 8192 with G % 128 == 0 (segment kernel, then the ring), M = 2 K = 4096 /
+# 4160 with G % 128 != 0 (row kernel, then the ring), M = 2 K = 2048 / 4096
+# with G = 128 (ring, then the segment kernel).
+@pytest.mark.parametrize("M,N,K,G", [
+    (1, 300, 8192, 32), (1, 300, 8448, 32), (1, 200, 16384, 32), (1, 200, 16512, 32),
+    (1, 8192, 8448, 128), (1, 8193, 8448, 128),
+    (2, 500, 4096, 64), (2, 500, 4160, 64), (2, 700, 2048, 128), (2, 700, 4096, 128),
+])
+def test_matvec_int4_route_limits(M, N, K, G):
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K + G)
+    got = _matvec(4, X, W, S, N, K, G, "f16")
+    _close(got, _oracle(4, X, W, S, G))
+
+
 # LDS-ring tile kernel with a partial last 512-byte row chunk (zeros past the
 # row end through out-of-range buffer offsets, activations zeroed past K).
 @pytest.mark.parametrize("wbits,M,N,K,G", [
