@@ -180,15 +180,35 @@ static int launch_gemv_seg_m(const void* X, const void* W, const void* S, void* 
   constexpr int rw = M_ <= 2 ? 4 : 2;
   if (nseg == 1) return launch_gemv_seg_t<M_, 1, rw * 2, SD, OD>(X, W, S, O, M, N, K, G, st);
   if (nseg == 2) return launch_gemv_seg_t<M_, 2, rw, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if constexpr (M_ == 1) {
+    // M = 1 runs 3 and 6 segments as such instead of padding to 4 / 8 (the
+    // padded segments' MFMAs and activation registers cost as much as real
+    // ones): 4096 x 6144 5.2 -> 4.7 us, 4096 x 11008 9.7 -> 7.3, 8192 x
+    // 11008 17.5 -> 11.8.  Two rows per wave from N = 4096 (4 at 3 segments
+    // from N = 8192) halve the workgroups, each of which builds the whole
+    // activation row (4096 x 14336: 10.1 -> 8.5 us).
+    if (nseg == 3) {
+      if (N >= 8192) return launch_gemv_seg_t<M_, 3, 4, SD, OD>(X, W, S, O, M, N, K, G, st);
+      return launch_gemv_seg_t<M_, 3, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+    }
+  }
   if constexpr (M_ <= 2) {
     if (nseg <= 4) return launch_gemv_seg_t<M_, 4, (rw > 2 ? rw / 2 : 1), SD, OD>(X, W, S, O, M, N, K, G, st);
   }
-  if constexpr (M_ == 1) return launch_gemv_seg_t<M_, 8, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+  if constexpr (M_ == 1) {
+    if (nseg <= 6) {
+      if (N >= 4096) return launch_gemv_seg_t<M_, 6, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+      return launch_gemv_seg_t<M_, 6, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+    }
+    if (N >= 4096) return launch_gemv_seg_t<M_, 8, 2, SD, OD>(X, W, S, O, M, N, K, G, st);
+    return launch_gemv_seg_t<M_, 8, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+  }
   return LQ_ERR_SHAPE;   // excluded by gemv_seg_ok
 }
 
 // The segment kernel: int4, M <= 4, G % 128 == 0, 2048 <= K <= 16384
-// (K / 2048 rounded up to 1, 2, 4 or 8 segments, the last possibly partial),
+// (K / 2048 rounded up to 1, 2, 4 or 8 segments, at M = 1 also 3 or 6; the
+// last possibly partial),
 // at most 8 (activation row, segment) pairs per lane (more spill registers);
 // buffer sizes plus the out-of-range offset within 32 bits.
 static bool gemv_seg_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t G) {
@@ -379,9 +399,12 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
     // 11008 x 4096: 8.1 against 8.8; at K = 2048, and at M = 3, 4 with
     // N >= 11008, the ring wins).
     const bool seg2 = WBITS == 4 && M == 2 && K >= 4096 && gemv_seg_ok(WBITS, M, N, K, G);
-    // int4 M = 1 with K > 8192: the segment kernel up to N = 8192 (4096 x
-    // 11008: 9.6 against 11.4 us), the ring beyond (11008 x 11008: 18 against 22)
-    const bool seg1 = WBITS == 4 && M == 1 && K > 8192 && N <= 8192 && gemv_seg_ok(WBITS, M, N, K, G);
+    // int4 M = 1 with K > 8192: the segment kernel at up to 6 segments for
+    // any N (4096 x 11008: 7.3 against 11.2 us, 11008 x 11008: 16.3 against
+    // 17.2, 14336 x 11008: 19.7 against 20.4), at 7 or 8 segments up to
+    // N = 8192 (4096 x 14336: 8.5 against 11.7), the ring beyond
+    const bool seg1 = WBITS == 4 && M == 1 && K > 8192 && (N <= 8192 || K <= 6 * 2048) &&
+                      gemv_seg_ok(WBITS, M, N, K, G);
     // int4 M = 1 with K > 8192 and groups the segment kernel cannot take
     // (G % 128 != 0): the row kernel at 8 segments (G = 32: 4096 x 11008 10.0
     // against 13.0 us, 11008 x 11008 21.7 against 31.3)

@@ -257,13 +257,17 @@ def test_matvec_int4_partial_segment(M, N, K, G):
 # Both sides of every int4 M <= 2 routing limit (the kernel choice changes at
 # each): M = 1 K = 8192 / 8448 (row kernel at 4 / 8 segments), K = 16384 /
 # 16512 (row kernel's last K, then the ring tile kernel), N = 8192 / 8193 at
-# K > 8192 with G % 128 == 0 (segment kernel, then the ring), M = 2 K = 4096 /
+# K > 12288 with G % 128 == 0 (segment kernel, then the ring), M = 2 K = 4096 /
 # 4160 with G % 128 != 0 (row kernel, then the ring), M = 2 K = 2048 / 4096
 # with G = 128 (ring, then the segment kernel).
 @pytest.mark.parametrize("M,N,K,G", [
     (1, 300, 8192, 32), (1, 300, 8448, 32), (1, 200, 16384, 32), (1, 200, 16512, 32),
-    (1, 8192, 8448, 128), (1, 8193, 8448, 128),
+    (1, 8192, 12416, 128), (1, 8193, 12416, 128), (1, 8193, 8448, 128),
     (2, 500, 4096, 64), (2, 500, 4160, 64), (2, 700, 2048, 128), (2, 700, 4096, 128),
+    # M = 1 segment counts 3 and 6 (1, 2, 4 rows per wave), 8 at 1 or 2 rows
+    # per wave, and N > 8192 on 6 segments / on the ring at 7
+    (1, 4096, 6144, 128), (1, 8192, 5120, 128), (1, 2000, 11008, 128), (1, 4100, 10240, 256),
+    (1, 11008, 11008, 128), (1, 4096, 14336, 128), (1, 300, 16384, 128), (1, 8200, 12416, 128),
 ])
 def test_matvec_int4_route_limits(M, N, K, G):
     X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K + G)
