@@ -132,7 +132,20 @@ static int launch_gemv_rows_m(const void* X, const void* W, const void* S, void*
   if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
   // (two activation rows x 2 segments: 210 VGPRs, sized for 2 workgroups per CU)
   if (nseg <= 2) return launch_gemv_rows_t<M_, 2, 4, SD, OD, EPI, M_ == 2 ? 2 : 3>(X, W, S, O, M, N, K, G, st);
+  // M = 1 runs 3 and 6 segments as such instead of padding to 4 / 8 (G = 32:
+  // 4096 x 6144 5.7 -> 4.8 us, 11008 x 6144 11.4 -> 9.0, 4096 x 11008
+  // 9.9 -> 8.5, 11008 x 11008 21.7 -> 18.4)
+  if constexpr (M_ == 1) {
+    if (nseg == 3) {
+      if (N >= 8192) return launch_gemv_rows_t<M_, 3, 4, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
+      return launch_gemv_rows_t<M_, 3, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+    }
+  }
   if (nseg <= 4) return launch_gemv_rows_t<M_, 4, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+  if constexpr (M_ == 1) {
+    // 6 segments: 181 VGPRs, sized for 2 workgroups per CU (3 measured slower)
+    if (nseg <= 6) return launch_gemv_rows_t<M_, 6, 2, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
+  }
   // 8 segments (K <= 16384, M = 1): 237 VGPRs, sized for 2 workgroups per CU
   return launch_gemv_rows_t<M_, 8, 2, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
 }

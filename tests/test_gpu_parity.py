@@ -268,6 +268,8 @@ def test_matvec_int4_partial_segment(M, N, K, G):
     # per wave, and N > 8192 on 6 segments / on the ring at 7
     (1, 4096, 6144, 128), (1, 8192, 5120, 128), (1, 2000, 11008, 128), (1, 4100, 10240, 256),
     (1, 11008, 11008, 128), (1, 4096, 14336, 128), (1, 300, 16384, 128), (1, 8200, 12416, 128),
+    # the row kernel (G % 128 != 0) at 3 (2 / 4 rows per wave) and 6 segments
+    (1, 4096, 6144, 32), (1, 8192, 5120, 64), (1, 2000, 11008, 32), (1, 5000, 12288, 96),
 ])
 def test_matvec_int4_route_limits(M, N, K, G):
     X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=M + N + K + G)
@@ -535,7 +537,9 @@ def _silu_mul_oracle(X, Wg, Sg, Wu, Su, G):
     (300, 1100, 512, 64, "f16"),    # prefill GEMM epilogue, ragged tiles
     (1100, 2048, 1024, 128, "f16"), # 256-row tiles
     (40, 300, 576, 32, "f16"),      # no fused kernel: staged fp32 matvec + pairwise epilogue
-    (1, 700, 11008, 32, "f16"),     # row kernel at 8 segments with the epilogue
+    (1, 700, 11008, 32, "f16"),     # row kernel at 6 segments with the epilogue
+    (1, 4100, 6144, 32, "f16"),     # row kernel at 3 segments, 4 rows per wave
+    (1, 300, 14336, 64, "f16"),     # row kernel at 8 segments
     (8, 100, 576, 64, "f16"),
 ])
 def test_matvec_int4_silu_mul(policy, M, I, K, G, xd):
