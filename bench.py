@@ -338,7 +338,7 @@ def profile_case(name, launches=50):
 
 SWEEP_M = (1, 2, 4, 8, 16, 32, 64, 96, 256, 1024)
 SWEEP_SHAPES = ((576, 576), (1536, 576), (576, 1536), (4096, 4096), (11008, 4096), (4096, 11008),
-                (14336, 4096))   # (N, K): SmolLM2-135M and LLaMA-7B-class linear layers
+                (14336, 4096), (4096, 14336))   # (N, K): SmolLM2-135M, LLaMA-7B / 8B-class linear layers
 
 
 def sweep():

@@ -25,6 +25,9 @@ int launch_generic(const void*, const void*, const void*, void*, int64_t, int64_
 template <int WBITS>
 int launch_gemm(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
                 int, int, hipStream_t, const FixedScratch*);
+template <int WBITS>
+int launch_gemm_split_only(const void*, const void*, const void*, void*, int64_t, int64_t,
+                           int64_t, int64_t, int, int, hipStream_t, const FixedScratch*);
 int launch_zero_fill(void*, int64_t, int, hipStream_t);
 int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
                     hipStream_t);
@@ -94,6 +97,17 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
     // Skinny (decode) kernel: 16-byte weight chunks per lane must lie in one
     // group and in one row.
     const int64_t lane_k = WBITS == 4 ? 32 : 16;
+    // 16 < M <= 64 (int8: 32 < M) at N = 4096-class widths with long rows:
+    // the GEMM with k split 8 ways fills the CUs, while the decode kernel
+    // streams the whole activation block per workgroup (1 x 4096 x 11008
+    // int4: 36.0 -> 28.6 us at M = 64, 27.1 -> 26.7 at M = 32; 4096 x 14336
+    // M = 64: 45.3 -> 33.7; int8 M = 64 34.2 -> 29.3).  The split needs its
+    // workspace; without one the decode kernel runs.
+    if (M > (WBITS == 4 ? 16 : 32) && M <= 64 && N > 3072 && N <= 4096 && K >= 10240 &&
+        K % 64 == 0 && (WBITS == 4 ? G % 32 == 0 : G % 64 == 0)) {
+      const int rc = launch_gemm_split_only<WBITS>(X, W, S, O, M, N, K, G, sd, od, st, fixed);
+      if (rc != LQ_ERR_SHAPE) return rc;
+    }
     if (M <= 64 && K % lane_k == 0 && G % lane_k == 0)
       return launch_skinny<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
     // Prefill MFMA GEMM: each loader thread's 32 k (int4) / 16 k (int8)

@@ -154,9 +154,11 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     }
   }
   const int row_bytes = WBITS == 4 ? (K >> 1) : K;
-  // split-K: workgroup row blockIdx.y covers k in [kbeg, kbeg + kspan) and
-  // writes its fp32 partial sums to slice blockIdx.y of O
+  // split-K: workgroup row blockIdx.y covers k in [kbeg, min(kbeg + kspan, K))
+  // (kspan a whole number of 64-k steps) and writes its fp32 partial sums to
+  // slice blockIdx.y of O
   const int kbeg = blockIdx.y * kspan;
+  kspan = min(kspan, K - kbeg);                // the last split may be shorter
   const size_t obase = size_t(blockIdx.y) * M * N;
   const int wrow0 = wm * TM * 16;              // first tile row this wave multiplies
 
@@ -486,6 +488,12 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #endif
 typedef GemmCfg<LQ_GEMM_CFG> GemmDefault;   // default: 256 x 128 tile, 4 x 2 waves of 64 x 64
 
+// k per split: the 64-k steps dealt in equal runs, the last run possibly
+// shorter (the kernel clamps it to K)
+static int64_t split_span(int64_t K, int splits) {
+  return (K / kBK + splits - 1) / splits * kBK;
+}
+
 template <class C, int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O, int64_t M,
                            int64_t N, int64_t K, int64_t G, int splits, hipStream_t st,
@@ -495,7 +503,7 @@ static int launch_gemm_cfg(const void* X, const void* W, const void* S, void* O,
   hipLaunchKernelGGL((gemm_w4_kernel<C, WBITS, SD, OD, EPI, XD>), dim3(unsigned(tiles_m * tiles_n), unsigned(splits)),
                      dim3(C::kThreads), 0, st, static_cast<const half_t*>(X),
                      static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K), int(K / G),
-                     int(G), tiles_m, tiles_n, int(K / splits), sd_rt, od_rt);
+                     int(G), tiles_m, tiles_n, int(split_span(K, splits)), sd_rt, od_rt);
   return check_launch();
 }
 
@@ -672,12 +680,25 @@ __global__ __launch_bounds__(256) void split_reduce_silu_kernel(const float* __r
 }
 
 // Number of k splits for `tiles` output tiles: the largest of 8, 6, 4, 3, 2
-// that keeps tiles x splits <= 256 (one workgroup per CU) and divides the
-// 64-k steps into runs of >= 4, and at least `need`.
-static int choose_splits(int64_t tiles, int64_t K, int need) {
+// that keeps tiles x splits <= 256 (one workgroup per CU), deals the 64-k
+// steps into runs of >= 4 (equal runs, the last one possibly shorter, as
+// split_span), keeps the scale groups any split touches within the staging
+// LDS when `post` (int8 / bf16 post-scales), and is at least `need`.
+// Uneven runs let step counts without a divisor use every CU (1 x 4096 x
+// 11008 tiles: 172 steps, 4 even splits -> 8).
+static int choose_splits(int64_t tiles, int64_t K, int64_t G, int need, bool post) {
   const int64_t ksteps = K / kBK;
   for (int s : {8, 6, 4, 3, 2}) {
-    if (s < need || tiles * s > 256 || ksteps % s != 0 || ksteps / s < 4) continue;
+    if (s < need || tiles * s > 256) continue;
+    const int64_t run = (ksteps + s - 1) / s;
+    if (run < 4 || ksteps - (s - 1) * run < 4) continue;
+    if (post) {
+      const int64_t span = run * kBK;
+      int64_t most = 0;
+      for (int64_t i = 0; i < s; ++i)
+        most = std::max(most, (std::min((i + 1) * span, K) - 1) / G - (i * span) / G + 1);
+      if (most > kGemmScaleFloats / 128) continue;
+    }
     return s;
   }
   return need;
@@ -737,7 +758,7 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
   }
   const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
                         ((N + GemmSmall::BN - 1) / GemmSmall::BN);
-  const int splits = choose_splits(tiles, K, need);
+  const int splits = choose_splits(tiles, K, G, need, WBITS == 8 || XD == LQ_BF16);
   if (splits > 1) {
     const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G,
                                                                         splits, st, fixed, sd_rt, od_rt);
@@ -764,6 +785,45 @@ int launch_gemm(const void* X, const void* W, const void* S, void* O, int64_t M,
 #undef LQ_GM
   return LQ_ERR_DTYPE;
 }
+
+// Decode-sized M (16 < M <= 64) on the split-K GEMM, for the callers whose
+// shapes it serves faster than the decode kernels (few 128-column tiles, long
+// rows): only when the k split applies (>= 2 splits and their workspace or
+// the caller's fixed scratch at hand); LQ_ERR_SHAPE otherwise, so the caller
+// takes its decode kernel instead of an unsplit GEMM of a few tiles.
+template <int WBITS>
+int launch_gemm_split_only(const void* X, const void* W, const void* S, void* O, int64_t M,
+                           int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st,
+                           const FixedScratch* fixed) {
+  const int need = min_splits<WBITS>(K, G);
+  if (need == 0 || K % kBK != 0) return LQ_ERR_SHAPE;
+  const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
+                        ((N + GemmSmall::BN - 1) / GemmSmall::BN);
+  const int splits = choose_splits(tiles, K, G, need, WBITS == 8);
+  if (splits < 2) return LQ_ERR_SHAPE;
+  int rc = LQ_ERR_DTYPE;
+#define LQ_GSO(SD_, OD_)                                                                  \
+  if (sd == SD_ && od == OD_)                                                             \
+    rc = launch_gemm_split<GemmSmall, WBITS, SD_, OD_>(X, W, S, O, M, N, K, G, splits, st, fixed)
+  LQ_GSO(LQ_F16, LQ_F16);
+  LQ_GSO(LQ_F16, LQ_F32);
+  LQ_GSO(LQ_F16, LQ_BF16);
+  LQ_GSO(LQ_F32, LQ_F16);
+  LQ_GSO(LQ_F32, LQ_F32);
+  LQ_GSO(LQ_F32, LQ_BF16);
+  LQ_GSO(LQ_BF16, LQ_F16);
+  LQ_GSO(LQ_BF16, LQ_F32);
+  LQ_GSO(LQ_BF16, LQ_BF16);
+#undef LQ_GSO
+  // (no launch happened for a workspace that is missing or too small)
+  return rc == LQ_ERR_SCRATCH ? LQ_ERR_SHAPE : rc;
+}
+template int launch_gemm_split_only<4>(const void*, const void*, const void*, void*, int64_t,
+                                       int64_t, int64_t, int64_t, int, int, hipStream_t,
+                                       const FixedScratch*);
+template int launch_gemm_split_only<8>(const void*, const void*, const void*, void*, int64_t,
+                                       int64_t, int64_t, int64_t, int, int, hipStream_t,
+                                       const FixedScratch*);
 
 // O [M, N / 2] = silu(P[:, 2i]) * P[:, 2i + 1] for an fp32 matvec result P.
 int launch_silu_pairs(const float* P, void* O, int64_t M, int64_t N, int od, hipStream_t st) {

@@ -102,6 +102,8 @@ def test_bf16_activations_shapes(wbits, M, N, K, G, sd, od):
     (8, 512, 4096, 4096, 128),
     (4, 96, 200, 1024, 64),
     (8, 300, 257, 2048, 2048),
+    (4, 100, 640, 4160, 64),      # split-K with a shorter last split
+    (8, 96, 1024, 11008, 128),
 ])
 def test_bf16_activations_prefill(wbits, M, N, K, G):
     """bf16 prefill on the MFMA GEMM (bf16 MFMAs on exact integer weights,

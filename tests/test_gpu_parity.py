@@ -198,7 +198,10 @@ def test_matvec_lds_ring_shapes(wbits, M, N, K, G):
     (17, 64, 1024, 64), (33, 300, 2048, 16), (64, 1000, 4096, 4096), (48, 4100, 1536, 512),
     (16, 1000, 4096, 4096), (3, 77, 1024, 1024), (32, 11008, 4096, 128), (64, 9000, 768, 32),
     (40, 500, 1536, 384), (24, 333, 3072, 768), (64, 14336, 4096, 4096), (12, 777, 2048, 512),
-    (9, 4100, 1024, 1024)])
+    (9, 4100, 1024, 1024),
+    # 16 < M <= 64 (int8: 32 < M) at N <= 4096 with long rows: the split-K
+    # GEMM (8 uneven splits of 172 / 160 / 224 steps)
+    (64, 4096, 11008, 128), (33, 4000, 10240, 64), (48, 4096, 14336, 14336), (20, 3100, 11008, 32)])
 def test_matvec_many_rows_and_per_channel(wbits, M, N, K, G):
     """Decode/verify sizes up to M = 64 and per-channel / large groups
     (one or few scales per row, whose scale rows are not 16-byte multiples).
@@ -361,9 +364,14 @@ def test_matvec_int4_bf16_scales_or_output(sd, od, M, N, K):
     (4, 128, 4096, 4096, 128, "f16"),    # 32 tiles, 8 splits
     (8, 128, 4096, 4096, 128, "f32"),
     (4, 300, 2048, 2048, 128, "f16"),    # 48 tiles, 4 splits
-    (8, 96, 4096, 11008, 128, "f16"),    # 86 scale groups > LDS: 4 splits, groups straddle splits
+    (8, 96, 4096, 11008, 128, "f16"),    # 86 scale groups > LDS: uneven splits, groups straddle splits
     (8, 256, 640, 4096, 4096, "f32"),    # per-channel: splits shorter than the group
     (8, 130, 384, 4096, 64, "f16"),      # 64 groups: fit without a forced split
+    # uneven runs (the last split shorter): 172 steps in 8, 65 in 6, 79 in 8
+    (4, 96, 4096, 11008, 32, "f16"),
+    (4, 100, 640, 4160, 32, "f32"),
+    (8, 200, 1000, 5056, 64, "f16"),     # int8 post-scales: groups straddle uneven splits
+    (8, 70, 4096, 14336 - 64, 14336 - 64, "f16"),   # per channel, 223 steps in 8
 ])
 def test_matmul_prefill_split_k(wbits, M, N, K, G, od):
     X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=M * 7 + N + K)
@@ -579,3 +587,45 @@ def test_matvec_int4_silu_mul_other_dtypes(M, I, K, G, xd, sd, od):
         bound = bound + 2.0 ** -8 * np.abs(want)
     err = np.abs(got - want)
     assert (err <= bound).all(), (err.max(), np.argmax(err - bound))
+
+
+def test_decode_gemm_route_in_graph_on_a_fresh_stream():
+    """16 < M <= 64 at N = 4096 with long rows takes the split-K GEMM only
+    when its workspace exists: a capture on a fresh stream (no workspace, no
+    allocation under capture) runs the decode kernel instead.  The graph is
+    replayed three times with eager calls (which take the GEMM) on the
+    default stream in between; every result must match the oracle."""
+    import ctypes
+
+    import torch
+
+    from locomp_amd import _lib
+
+    lib = _lib.load()
+    vp = ctypes.c_void_p
+    M, N, K, G = 48, 4096, 11008, 128
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=91)
+    want = _oracle(4, X, W, S, G)
+    Xd, Wd, Sd = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (X, W, S))
+    Od = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    Oe = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+
+    def call(out, stream):
+        return lib.locomp_amd_dequant_matvec_int4(
+            vp(Xd.data_ptr()), vp(Wd.data_ptr()), vp(Sd.data_ptr()), vp(out.data_ptr()), K, K // 2,
+            K // G, G, N, M, _lib.F16, _lib.F16, _lib.F16, vp(stream.cuda_stream))
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        assert call(Od, s) == 0
+    torch.cuda.synchronize()
+    for _ in range(3):
+        Od.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert call(Oe, torch.cuda.current_stream()) == 0   # eager work between replays
+        torch.cuda.synchronize()
+        _close(Od.cpu().numpy(), want)
+        _close(Oe.cpu().numpy(), want)

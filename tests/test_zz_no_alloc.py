@@ -38,6 +38,7 @@ CASES = [
     ((128, 4096, 4096, 128), (100, 2048, 4096, 128)),   # 8-way split, then 4-way
     ((512, 4096, 4096, 128), (200, 1024, 2048, 64)),
     ((1, 11008, 4096, 128), (4, 4096, 4096, 32)),
+    ((64, 4096, 11008, 128), (24, 4096, 10240, 32)),   # decode M on the split-K GEMM, uneven runs
 ]
 
 
