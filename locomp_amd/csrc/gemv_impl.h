@@ -425,7 +425,13 @@ static int launch_skinny_sd_od(const void* X, const void* W, const void* S, void
     // int4 M = 2 with G % 128 != 0 and K <= 4096: the row kernel (G = 32:
     // 11008 x 4096 9.0 against 13.0 us, 4096 x 4096 5.0 against 7.1)
     const bool rows2 = WBITS == 4 && M == 2 && G % 128 != 0 && gemv_rows_ok(WBITS, M, K, G);
-    if (!seg2 && !seg1 && !rows1 && !rows2 && (M >= 2 || WBITS == 8 || K > 8192) &&
+    // int4 M = 3, 4 with N <= 2048 and 2048 < K <= 4096: the segment kernel
+    // (the ring has at most 128 one-tile workgroups there: 1024 x 4096 5.3
+    // against 4.5 us, 2048 x 4096 5.4 against 4.5; at K = 2048 or N = 3072
+    // the ring wins); fp16 scales / outputs only (its M = 4 instantiation)
+    const bool seg34 = WBITS == 4 && SD != LQ_BF16 && OD != LQ_BF16 && (M == 3 || M == 4) &&
+                       N <= 2048 && K > 2048 && K <= 4096 && gemv_seg_ok(WBITS, M, N, K, G);
+    if (!seg2 && !seg1 && !rows1 && !rows2 && !seg34 && (M >= 2 || WBITS == 8 || K > 8192) &&
         gemv_tile_ok(WBITS, M, N, K, G, SD == LQ_F32 ? 4 : 2))
       return launch_gemv_tile<WBITS, SD, OD>(X, W, S, O, M, N, K, G, st);
   }

@@ -271,6 +271,9 @@ def test_matvec_int4_partial_segment(M, N, K, G):
     # per wave, and N > 8192 on 6 segments / on the ring at 7
     (1, 4096, 6144, 128), (1, 8192, 5120, 128), (1, 2000, 11008, 128), (1, 4100, 10240, 256),
     (1, 11008, 11008, 128), (1, 4096, 14336, 128), (1, 300, 16384, 128), (1, 8200, 12416, 128),
+    # M = 3, 4 at N <= 2048, 2048 < K <= 4096: the segment kernel (M = 4
+    # instantiation), the ring at N = 2049 and at K = 2048
+    (3, 1024, 4096, 128), (4, 2048, 3072, 256), (4, 2049, 4096, 128), (4, 1000, 2048, 128),
     # the row kernel (G % 128 != 0) at 3 (2 / 4 rows per wave) and 6 segments
     (1, 4096, 6144, 32), (1, 8192, 5120, 64), (1, 2000, 11008, 32), (1, 5000, 12288, 96),
 ])
