@@ -91,8 +91,13 @@ static int launch_seg_x(const void* X, const void* W, const void* S, void* O, in
   if (xd == LQ_BF16) {
     if (nseg == 1) launch_seg_x_t<1, 8, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
     else if (nseg == 2) launch_seg_x_t<2, 4, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
-    else if (nseg <= 4) launch_seg_x_t<4, 2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
-    else launch_seg_x_t<8, 1, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+    // 3 and 6 segments as such (not padded to 4 / 8), 2 rows per wave from
+    // 3 segments (4096 x 6144 5.8 -> 4.9 us, 4096 x 11008 12.2 -> 7.8,
+    // 11008 x 11008 28.5 -> 18.5, 4096 x 14336 12.5 -> 10.6)
+    else if (nseg == 3) launch_seg_x_t<3, 2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+    else if (nseg == 4) launch_seg_x_t<4, 2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+    else if (nseg <= 6) launch_seg_x_t<6, 2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+    else launch_seg_x_t<8, 2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
   } else {
     if (nseg == 1) launch_seg_x_t<1, 8, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
     else if (nseg == 2) launch_seg_x_t<2, 4, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);

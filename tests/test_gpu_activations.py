@@ -87,6 +87,9 @@ def test_bf16_activations_cfg3(wbits, M):
     (8, 7, 333, 2064, 16),       # partial chunk, 16-k groups
     (8, 16, 130, 11008, 128),
     (8, 2, 64, 1536, 64),
+    (4, 1, 300, 6144, 128),      # segment kernel at 3 / 6 / 8 segments, 2 rows per wave
+    (4, 1, 257, 11008, 128),
+    (4, 1, 130, 14336, 256),
 ])
 @pytest.mark.parametrize("sd,od", [("f16", "f16"), ("bf16", "bf16"), ("f32", "f32"), ("f16", "bf16")])
 def test_bf16_activations_shapes(wbits, M, N, K, G, sd, od):
