@@ -83,7 +83,8 @@ static void launch_seg_x_t(const void* X, const void* W, const void* S, void* O,
 }
 
 // M = 1, int4, G % 128: the 2048-k segment kernel (bf16 up to 8 segments,
-// fp32 - three operand sets per segment - up to 2); LQ_ERR_SHAPE otherwise.
+// fp32 - three operand sets per segment - up to 2, 3 at N <= 4096);
+// LQ_ERR_SHAPE otherwise.
 static int launch_seg_x(const void* X, const void* W, const void* S, void* O, int64_t M,
                         int64_t N, int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
   const int64_t nseg = (K + 2047) / 2048;
@@ -101,6 +102,10 @@ static int launch_seg_x(const void* X, const void* W, const void* S, void* O, in
   } else {
     if (nseg == 1) launch_seg_x_t<1, 8, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
     else if (nseg == 2) launch_seg_x_t<2, 4, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
+    // 3 segments (200 VGPRs at 2 rows per wave) up to N = 4096 (4096 x 6144
+    // 9.5 -> 7.3 us against the pre-split ring; at N = 11008 the ring wins,
+    // 14.0 against 16.1; 4 segments spill or lose)
+    else if (nseg == 3 && N <= 4096) launch_seg_x_t<3, 2, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
     else return LQ_ERR_SHAPE;
   }
   return check_launch();

@@ -148,7 +148,8 @@ def test_fp32_activations_cfg3(wbits, M):
 
 @pytest.mark.parametrize("wbits,M,N,K,G,sd", [
     (4, 1, 333, 2048, 32, "f16"), (4, 4, 100, 11008, 128, "f32"), (4, 3, 640, 4096, 64, "bf16"),
-    (8, 2, 257, 2064, 16, "f32"), (8, 4, 96, 4096, 4096, "f16"), (8, 1, 1000, 1024, 128, "f32")])
+    (8, 2, 257, 2064, 16, "f32"), (8, 4, 96, 4096, 4096, "f16"), (8, 1, 1000, 1024, 128, "f32"),
+    (4, 1, 4096, 6144, 128, "f16"), (4, 1, 300, 5120, 256, "f32"), (4, 1, 4097, 6144, 128, "f32")])
 def test_fp32_activations_shapes(wbits, M, N, K, G, sd):
     X, W, S = _case(wbits, M, N, K, G, seed=M + N + K)
     X = X * np.float32(3.0)   # values across several binades
