@@ -20,9 +20,10 @@
  *   - All pointers are device pointers.  The library allocates only
  *     grow-only workspaces per (device, stream): on the first prefill that
  *     splits K, on the first SiLU * mul call without a fused kernel, and on
- *     the first fp32-activation decode call at M <= 4 (its bf16 part rows,
- *     24 K bytes); they are held until the process ends or
- *     locomp_amd_release_workspaces.
+ *     the first fp32-activation call (its bf16 part rows: 24 K bytes at
+ *     M <= 4; at M > 4 3 M K x 2 bytes plus the parts' fp32 products,
+ *     3 M N x 4 bytes, each at most 256 MB, larger M in row blocks); they
+ *     are held until the process ends or locomp_amd_release_workspaces.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
  *     is asynchronous: the caller synchronises.
  *   - Return value: 0 on success; a negative LQ_ERR_* for invalid arguments
@@ -126,7 +127,11 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * bf16 run on fp16 / bf16 matrix cores at every M; fp32 at M <= 4 runs on
  * bf16 matrix cores as three exact bf16 parts (split once per call into a
  * workspace, or inside the kernel on a capturing stream that has none yet);
- * other fp32 shapes take a generic kernel.  The fast kernels need X and W 16-byte aligned and the
+ * fp32 at M > 4 is split the same way into 3 M bf16 rows that take the bf16
+ * route (3 M <= 16: the decode kernel; else the MFMA GEMM, G % 64 == 0)
+ * with fp32 products, whose three part rows are then added; other fp32
+ * shapes, and a capture on a stream without those workspaces, take a
+ * generic kernel.  The fast kernels need X and W 16-byte aligned and the
  * scales 4-byte aligned (otherwise a generic kernel runs).
  * A prefill GEMM with fewer output tiles than CUs splits K and keeps an fp32
  * workspace per (device, stream), allocated on first use and held until the

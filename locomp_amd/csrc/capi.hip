@@ -1,5 +1,6 @@
 // C ABI entry points: argument validation and kernel selection.
 // Declarations and conventions: include/locomp_amd.h.
+#include <algorithm>
 #include <atomic>
 #include <string>
 
@@ -29,6 +30,8 @@ template <int WBITS>
 int launch_gemm_split_only(const void*, const void*, const void*, void*, int64_t, int64_t,
                            int64_t, int64_t, int, int, hipStream_t, const FixedScratch*);
 int launch_zero_fill(void*, int64_t, int, hipStream_t);
+int launch_split_f32_rows(const float*, void*, int64_t, int64_t, hipStream_t);
+int launch_sum_part_rows(const float*, void*, int64_t, int64_t, int, hipStream_t);
 int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
                     hipStream_t);
 int launch_silu_fast(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
@@ -63,13 +66,52 @@ static bool fast_allowed() { return g_policy.load(std::memory_order_relaxed) == 
 
 using namespace lq;
 
+template <int WBITS>
+static int matmul_dispatch(const void* X, const void* W, const void* S, void* O, int64_t K,
+                           int64_t G, int64_t N, int64_t M, int xd, int sd, int od, hipStream_t st,
+                           const FixedScratch* fixed = nullptr);
+
+// fp32 activations at M > 4: each row split exactly into three bf16 parts
+// (hi + mid + lo, as the M <= 4 kernels do), stacked as 3 M bf16 rows in the
+// stream's workspace slot 2, run through the bf16 route with fp32 output
+// (slot 3), and the three part rows' products added in order.  Each part
+// times an integer weight is exact in fp32, so the result is an fp32 dot
+// product in a different summation order.  Taken only where the bf16 route
+// is a fast one (3 M <= 16: the tile kernel; else the MFMA GEMM, G % 64),
+// in row blocks whose buffers fit the workspace cap; LQ_ERR_SHAPE (the
+// caller falls back) when it does not apply or a workspace is missing (a
+// capture on a stream that has none yet).
+template <int WBITS>
+static int matmul_f32_stacked(const void* X, const void* W, const void* S, void* O, int64_t K,
+                              int64_t G, int64_t N, int64_t M, int sd, int od, hipStream_t st) {
+  if (3 * M > 16 && (G % 64 != 0 || K % 64 != 0)) return LQ_ERR_SHAPE;
+  constexpr int64_t kCap = int64_t(256) << 20;          // bytes per workspace slot
+  const int64_t rows = std::max<int64_t>(1, std::min(kCap / (3 * K * 2), kCap / (3 * N * 4)));
+  const int64_t mb = std::min(M, rows);
+  void* parts = stream_workspace(2, size_t(3 * mb * K * 2), st);
+  void* prod = stream_workspace(3, size_t(3 * mb * N * 4), st);
+  if (parts == nullptr || prod == nullptr) return LQ_ERR_SHAPE;
+  const size_t osz = od == LQ_F32 ? 4 : 2;
+  for (int64_t m0 = 0; m0 < M; m0 += mb) {
+    const int64_t m = std::min(mb, M - m0);
+    int rc = launch_split_f32_rows(static_cast<const float*>(X) + m0 * K, parts, m, K, st);
+    if (rc != LQ_OK) return rc;
+    rc = matmul_dispatch<WBITS>(parts, W, S, prod, K, G, N, 3 * m, LQ_BF16, sd, LQ_F32, st);
+    if (rc != LQ_OK) return rc;
+    rc = launch_sum_part_rows(static_cast<const float*>(prod),
+                              static_cast<uint8_t*>(O) + size_t(m0 * N) * osz, m, N, od, st);
+    if (rc != LQ_OK) return rc;
+  }
+  return LQ_OK;
+}
+
 // Kernel choice for the dequant-matmul entries (WBITS = 4 or 8).
 // `fixed`: scratch lent by the caller for split-K partials (no allocation);
 // nullptr = the per-stream workspace.
 template <int WBITS>
 static int matmul_dispatch(const void* X, const void* W, const void* S, void* O, int64_t K,
                            int64_t G, int64_t N, int64_t M, int xd, int sd, int od, hipStream_t st,
-                           const FixedScratch* fixed = nullptr) {
+                           const FixedScratch* fixed) {
   if (!dtype_ok(xd) || !dtype_ok(sd) || !dtype_ok(od)) return LQ_ERR_DTYPE;
   if (M < 0) return LQ_ERR_SHAPE;
   if (M == 0 || N == 0) return LQ_OK;
@@ -85,6 +127,11 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
   if (fast_common && (xd == LQ_BF16 || xd == LQ_F32) && M <= 16) {
     // bf16 activations (M <= 16) and fp32 (M <= 4) on bf16 MFMAs
     const int rc = launch_skinny_x<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st, fixed);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
+  if (fast_common && xd == LQ_F32 && M > 4 && fixed == nullptr) {
+    // fp32 beyond the decode kernels' 4 rows: exact bf16 parts on the bf16 route
+    const int rc = matmul_f32_stacked<WBITS>(X, W, S, O, K, G, N, M, sd, od, st);
     if (rc != LQ_ERR_SHAPE) return rc;
   }
   if (fast_common && xd == LQ_BF16 && M > 16 && K % 64 == 0) {

@@ -8,13 +8,14 @@ namespace lq {
 
 void* stream_workspace(int slot, size_t bytes, hipStream_t st);
 
-// fp32 activations X [M, K] (M <= 4) -> their exact three-way bf16 split,
-// P [12, K] bf16 with row m + 4 part = part `part` of row m (rows of m >= M
-// are not written; the tile kernel does not read them).  Thread i takes 8
+// fp32 activations X [M, K] -> their exact three-way bf16 split, P bf16 with
+// row m + pstride * part = part `part` of row m (pstride 4 for the tile
+// kernel's 12 part rows at M <= 4: rows of m >= M are not written and not
+// read; pstride M for the stacked [3 M, K] layout).  Thread i takes 8
 // consecutive k of one row.
 static __global__ __launch_bounds__(256) void split_f32_parts_kernel(const float* __restrict__ X,
                                                              uint16_t* __restrict__ P, int M,
-                                                             int K) {
+                                                             int K, int pstride) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int per_row = K >> 3;
   if (i >= M * per_row) return;
@@ -29,8 +30,18 @@ static __global__ __launch_bounds__(256) void split_f32_parts_kernel(const float
     for (int e = 0; e < 8; ++e) h[e] = f32_part_bits(x[e], p) >> 16;
     const u32x4_t v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
                        h[6] | (h[7] << 16)};
-    *reinterpret_cast<u32x4_t*>(P + size_t(m + 4 * p) * K + k) = v;
+    *reinterpret_cast<u32x4_t*>(P + (size_t(m) + size_t(pstride) * p) * K + k) = v;
   }
+}
+
+// O [M, N] = P[0] + P[1] + P[2] (the three part rows' fp32 products, [3, M, N],
+// added in that order), stored as od.
+static __global__ __launch_bounds__(256) void sum_part_rows_kernel(const float* __restrict__ P,
+                                                           void* __restrict__ O, int64_t MN,
+                                                           int od) {
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= MN) return;
+  store_out<kRT>(O, size_t(e), (P[e] + P[MN + e]) + P[2 * MN + e], od);
 }
 
 template <int WBITS, int XD, int NSC>
@@ -145,7 +156,7 @@ int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_
   if (parts) {
     const int threads = int(M * (K / 8));
     hipLaunchKernelGGL(split_f32_parts_kernel, dim3((threads + 255) / 256), dim3(256), 0, st,
-                       static_cast<const float*>(X), static_cast<uint16_t*>(parts), int(M), int(K));
+                       static_cast<const float*>(X), static_cast<uint16_t*>(parts), int(M), int(K), 4);
     X = parts;
     LQ_NSC(kXPre)
   } else if (xd == LQ_BF16) {

@@ -157,6 +157,34 @@ def test_fp32_activations_shapes(wbits, M, N, K, G, sd):
     _close32(got, _oracle(wbits, X, W, _used(S, sd), G))
 
 
+@pytest.mark.parametrize("wbits,M,N,K,G,sd", [
+    (4, 5, 300, 2048, 64, "f16"),       # 15 part rows: the tile kernel
+    (4, 6, 257, 4096, 128, "f32"),      # 18 part rows: the bf16 GEMM (split K)
+    (8, 16, 1000, 1024, 128, "bf16"),
+    (4, 64, 1000, 4096, 128, "f16"),
+    (8, 300, 640, 2048, 256, "f32"),
+    (4, 2048, 4096, 4096, 128, "f16"),  # BASELINE cfg 5a shape with fp32 activations
+    (4, 8, 256, 512, 32, "f16"),        # G % 64 != 0: no fast bf16 route (generic kernel)
+])
+def test_fp32_activations_beyond_four_rows(wbits, M, N, K, G, sd):
+    """fp32 activations at M > 4: exact bf16 parts stacked as 3 M rows on the
+    bf16 route (tile kernel or MFMA GEMM) with fp32 products, the three part
+    rows added; full output against the oracle at rtol 1e-4."""
+    X, W, S = _case(wbits, M, N, K, G, seed=M + N + K + wbits)
+    X = X * np.float32(3.0)
+    got = _run(wbits, X, W, S, N, K, G, "f32", sd, "f32")
+    _close32(got, _oracle(wbits, X, W, _used(S, sd), G))
+
+
+@pytest.mark.parametrize("od", ["f16", "bf16"])
+def test_fp32_activations_beyond_four_rows_low_precision_out(od):
+    M, N, K, G = 40, 700, 2048, 128
+    X, W, S = _case(4, M, N, K, G, seed=5)
+    got = _run(4, X, W, S, N, K, G, "f32", "f16", od)
+    want = _oracle(4, X, W, _used(S, "f16"), G)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+
+
 def test_fp32_split_is_exact_on_hard_values():
     """Activations with 24 significant bits, tiny and huge magnitudes: the
     three-part split must reproduce fp32 products (one weight row of ones,
@@ -228,3 +256,51 @@ def test_fp32_activations_in_graph_on_a_fresh_stream():
         torch.cuda.synchronize()
         _close32(Od.cpu().numpy(), want)
         _close32(Oe.cpu().numpy(), want)
+
+
+def test_fp32_activations_beyond_four_rows_in_graph():
+    """fp32 at M > 4 needs two workspaces (part rows, fp32 products): a
+    capture on a stream that has none takes the generic kernel; after an
+    eager call on the same stream the capture takes the split route.  Both
+    graphs are replayed three times with eager work in between, every result
+    against the oracle."""
+    import ctypes
+
+    import torch
+
+    from locomp_amd import _lib
+
+    lib = _lib.load()
+    vp = ctypes.c_void_p
+    M, N, K, G = 8, 256, 512, 128
+    X, W, S = _case(4, M, N, K, G, seed=78)
+    want = _oracle(4, X, W, S, G)
+    Xd, Wd, Sd = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (X, W, S))
+    Oe = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+
+    def call(out, stream):
+        return lib.locomp_amd_dequant_matvec_int4(
+            vp(Xd.data_ptr()), vp(Wd.data_ptr()), vp(Sd.data_ptr()), vp(out.data_ptr()), K, K // 2,
+            K // G, G, N, M, _lib.F32, _lib.F32, _lib.F32, vp(stream.cuda_stream))
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    for warm in (False, True):
+        Od = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+        if warm:
+            with torch.cuda.stream(s):
+                assert call(Od, s) == 0   # sizes the stream's workspaces
+            torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            assert call(Od, s) == 0
+        torch.cuda.synchronize()
+        for _ in range(3):
+            Od.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert call(Oe, torch.cuda.current_stream()) == 0
+            torch.cuda.synchronize()
+            _close32(Od.cpu().numpy(), want)
+            _close32(Oe.cpu().numpy(), want)
+        del g
