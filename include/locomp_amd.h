@@ -128,7 +128,7 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * bf16 matrix cores as three exact bf16 parts (split once per call into a
  * workspace, or inside the kernel on a capturing stream that has none yet);
  * fp32 at M > 4 is split the same way into 3 M bf16 rows that take the bf16
- * route (3 M <= 16: the decode kernel; else the MFMA GEMM, G % 64 == 0)
+ * route (3 M <= 16: the decode kernel; else the MFMA GEMM, G % 32 == 0)
  * with fp32 products, whose three part rows are then added; other fp32
  * shapes, and a capture on a stream without those workspaces, take a
  * generic kernel.  The fast kernels need X and W 16-byte aligned and the

@@ -77,14 +77,14 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
 // (slot 3), and the three part rows' products added in order.  Each part
 // times an integer weight is exact in fp32, so the result is an fp32 dot
 // product in a different summation order.  Taken only where the bf16 route
-// is a fast one (3 M <= 16: the tile kernel; else the MFMA GEMM, G % 64),
+// is a fast one (3 M <= 16: the tile kernel; else the MFMA GEMM, G % 32),
 // in row blocks whose buffers fit the workspace cap; LQ_ERR_SHAPE (the
 // caller falls back) when it does not apply or a workspace is missing (a
 // capture on a stream that has none yet).
 template <int WBITS>
 static int matmul_f32_stacked(const void* X, const void* W, const void* S, void* O, int64_t K,
                               int64_t G, int64_t N, int64_t M, int sd, int od, hipStream_t st) {
-  if (3 * M > 16 && (G % 64 != 0 || K % 64 != 0)) return LQ_ERR_SHAPE;
+  if (3 * M > 16 && (G % 32 != 0 || K % 64 != 0)) return LQ_ERR_SHAPE;
   constexpr int64_t kCap = int64_t(256) << 20;          // bytes per workspace slot
   const int64_t rows = std::max<int64_t>(1, std::min(kCap / (3 * K * 2), kCap / (3 * N * 4)));
   const int64_t mb = std::min(M, rows);
@@ -135,7 +135,7 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
     if (rc != LQ_ERR_SHAPE) return rc;
   }
   if (fast_common && xd == LQ_BF16 && M > 16 && K % 64 == 0) {
-    // bf16 prefill: the MFMA GEMM on exact integer weights (G % 64)
+    // bf16 prefill: the MFMA GEMM on exact integer weights (G % 32)
     const int rc = launch_gemm_x<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st, fixed);
     if (rc != LQ_ERR_SHAPE) return rc;
   }
@@ -151,7 +151,7 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
     // M = 64: 45.3 -> 33.7; int8 M = 64 34.2 -> 29.3).  The split needs its
     // workspace; without one the decode kernel runs.
     if (M > (WBITS == 4 ? 16 : 32) && M <= 64 && N > 3072 && N <= 4096 && K >= 10240 &&
-        K % 64 == 0 && (WBITS == 4 ? G % 32 == 0 : G % 64 == 0)) {
+        K % 64 == 0 && G % 32 == 0) {
       const int rc = launch_gemm_split_only<WBITS>(X, W, S, O, M, N, K, G, sd, od, st, fixed);
       if (rc != LQ_ERR_SHAPE) return rc;
     }
@@ -159,10 +159,10 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
       return launch_skinny<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
     // Prefill MFMA GEMM: each loader thread's 32 k (int4) / 16 k (int8)
     // inside one group.
-    // int8 post-scales per group: whole 64-k steps per group (scale rows
+    // int8 post-scales per group: whole 32-k halves per group (scale rows
     // beyond what LDS holds split K; a shape no split fits, or a capturing
     // stream without the workspace that needs, takes the generic kernel).
-    const bool gemm_ok = WBITS == 4 ? G % 32 == 0 : G % 64 == 0;
+    const bool gemm_ok = G % 32 == 0;
     if (M > 64 && K % 64 == 0 && gemm_ok) {
       const int rc = launch_gemm<WBITS>(X, W, S, O, M, N, K, G, sd, od, st, fixed);
       if (rc != LQ_ERR_SHAPE) return rc;

@@ -368,6 +368,24 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     for (int i = 0; i < TM; ++i)
       fa[i] = *reinterpret_cast<const h8*>(as_l + a_lds_off(wrow0 + i * 16 + r16, kk * 4 + q4));
   };
+  // acc += part * s[n, g]; part = 0, for the group holding split-relative k
+  // `kin` (the first k of the half that ends it)
+  const bool half_groups = group % kBK != 0;
+  auto post_scale = [&](int kin) {
+    const int ns = (kbeg + kspan - 1) / group - kbeg / group + 1;
+    const int g = (kbeg + kin) / group - kbeg / group;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const float sj = Ssh[((wn * TN + j) * 16 + r16) * ns + g];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        acc[i][j] += part[i][j] * sj;
+        part[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+        // keep the MFMA-result read in this block (see the decode GEMV)
+        __asm__ volatile("" : "+v"(acc[i][j]), "+v"(part[i][j]));
+      }
+    }
+  };
   auto mfmas = [&](const h8 (&fa)[TM], const h8 (&fb)[TN]) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -415,26 +433,16 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     __syncthreads();
     read_frags(a_next, b_stage ^ 1, 0, fa0, fb0);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kPost) {
+      // groups of an odd number of 32-k halves (G % 64 == 32) may end after
+      // the first half: fold its sums before the second half's MFMAs
+      if (half_groups && (kbeg + ks * kBK + kBK / 2) % group == 0) post_scale(ks * kBK);
+    }
     mfmas(fa1, fb1);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kPost) {
-      // a group (or this split's share of one) ends with this step:
-      // acc += part * s[n, g]; part = 0
-      if ((kbeg + (ks + 1) * kBK) % group == 0 || ks + 1 == ksteps) {
-        const int ns = (kbeg + kspan - 1) / group - kbeg / group + 1;
-        const int g = (kbeg + ks * kBK) / group - kbeg / group;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const float sj = Ssh[((wn * TN + j) * 16 + r16) * ns + g];
-#pragma unroll
-          for (int i = 0; i < TM; ++i) {
-            acc[i][j] += part[i][j] * sj;
-            part[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-            // keep the MFMA-result read in this block (see the decode GEMV)
-            __asm__ volatile("" : "+v"(acc[i][j]), "+v"(part[i][j]));
-          }
-        }
-      }
+      // a group (or this split's share of one) ends with this step
+      if ((kbeg + (ks + 1) * kBK) % group == 0 || ks + 1 == ksteps) post_scale(ks * kBK + kBK / 2);
     }
     if constexpr (kBSets == 2) {
       __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kADma) : "memory");   // B(ks + 2) landed
@@ -860,7 +868,7 @@ template <int WBITS>
 int launch_gemm_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
                   int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st,
                   const FixedScratch* fixed) {
-  if (xd != LQ_BF16 || G % kBK != 0) return LQ_ERR_SHAPE;
+  if (xd != LQ_BF16 || G % (kBK / 2) != 0) return LQ_ERR_SHAPE;
   return launch_gemm_t<WBITS, kRT, kRT, false, LQ_BF16>(X, W, S, O, M, N, K, G, st, fixed, sd, od);
 }
 template int launch_gemm_x<4>(const void*, const void*, const void*, void*, int64_t, int64_t,

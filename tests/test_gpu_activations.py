@@ -107,6 +107,10 @@ def test_bf16_activations_shapes(wbits, M, N, K, G, sd, od):
     (8, 300, 257, 2048, 2048),
     (4, 100, 640, 4160, 64),      # split-K with a shorter last split
     (8, 96, 1024, 11008, 128),
+    (4, 2048, 1536, 576, 32),     # G = 32 (SmolLM2): scales after each 32-k half
+    (8, 200, 500, 2048, 32),
+    (4, 300, 700, 1536, 96),      # G = 96: groups end mid-step
+    (8, 130, 4096, 4096, 32),     # 128 groups: split K so each split's groups fit LDS
 ])
 def test_bf16_activations_prefill(wbits, M, N, K, G):
     """bf16 prefill on the MFMA GEMM (bf16 MFMAs on exact integer weights,
@@ -164,7 +168,8 @@ def test_fp32_activations_shapes(wbits, M, N, K, G, sd):
     (4, 64, 1000, 4096, 128, "f16"),
     (8, 300, 640, 2048, 256, "f32"),
     (4, 2048, 4096, 4096, 128, "f16"),  # BASELINE cfg 5a shape with fp32 activations
-    (4, 8, 256, 512, 32, "f16"),        # G % 64 != 0: no fast bf16 route (generic kernel)
+    (4, 8, 256, 512, 32, "f16"),        # G = 32: the GEMM scales after each 32-k half
+    (8, 40, 300, 1152, 96, "f32"),      # G = 96: groups end mid-step and at step ends
 ])
 def test_fp32_activations_beyond_four_rows(wbits, M, N, K, G, sd):
     """fp32 activations at M > 4: exact bf16 parts stacked as 3 M rows on the

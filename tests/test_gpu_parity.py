@@ -370,6 +370,9 @@ def test_matvec_int4_bf16_scales_or_output(sd, od, M, N, K):
     (8, 96, 4096, 11008, 128, "f16"),    # 86 scale groups > LDS: uneven splits, groups straddle splits
     (8, 256, 640, 4096, 4096, "f32"),    # per-channel: splits shorter than the group
     (8, 130, 384, 4096, 64, "f16"),      # 64 groups: fit without a forced split
+    # int8 with G % 64 == 32 (scales after a 32-k half), split and unsplit
+    (8, 100, 640, 1536, 32, "f16"),
+    (8, 2048, 1024, 1920, 96, "f16"),
     # uneven runs (the last split shorter): 172 steps in 8, 65 in 6, 79 in 8
     (4, 96, 4096, 11008, 32, "f16"),
     (4, 100, 640, 4160, 32, "f32"),
