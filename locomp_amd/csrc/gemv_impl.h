@@ -107,13 +107,14 @@ static int launch_gemv_lds_p(const void* X, const void* W, const void* S, void* 
 }
 
 
-template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3>
+template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3, int XD = LQ_F16>
 static int launch_gemv_rows_t(const void* X, const void* W, const void* S, void* O, int64_t M,
-                              int64_t N, int64_t K, int64_t G, hipStream_t st) {
+                              int64_t N, int64_t K, int64_t G, hipStream_t st, int sd_rt = 0,
+                              int od_rt = 0) {
   const unsigned blocks = unsigned((N + 4 * RW - 1) / (4 * RW));
-  hipLaunchKernelGGL((gemv_rows_kernel<M_, NSEG, RW, SD, OD, EPI, OCC>), dim3(blocks), dim3(256), 0, st,
-                     static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
-                     int(N), int(K), int(K / G), int(G));
+  hipLaunchKernelGGL((gemv_rows_kernel<M_, NSEG, RW, SD, OD, EPI, OCC, XD>), dim3(blocks), dim3(256), 0,
+                     st, X, static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K), int(K / G),
+                     int(G), sd_rt, od_rt);
   return check_launch();
 }
 

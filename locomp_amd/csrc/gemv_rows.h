@@ -21,11 +21,24 @@ namespace lq {
 // up_i) and the kernel stores silu(gate_i) * up_i to O [M, N / 2] instead of
 // the N dot products (examples/54_smollm2_inference.py:113-120, 545-548).
 // OCC: workgroups per CU the register budget is sized for (2 for 8 segments).
-template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3>
+// XD: activation dtype.  bf16 takes the weights decoded to bf16 128 + q
+// (0x4300 | q) and v_dot2_f32_bf16 (exact products, fp32 sums), the bias
+// 136 x the activation sum; fp32 takes three exact bf16 parts per activation
+// (hi + mid + lo), three dot products per weight pair.  SD / OD = kRT take
+// the scale / output dtypes from sd_rt / od_rt.
+template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3, int XD = LQ_F16>
 __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
-    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
-    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
-  typedef typename Elem<SD>::T stype;
+    const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
+    int od_rt = 0) {
+  typedef typename Elem<SD == kRT ? LQ_F32 : SD>::T stype;   // (kRT: converted at load)
+  constexpr bool kH = XD == LQ_F16;
+  constexpr int NP = XD == LQ_F32 ? 3 : 1;      // bf16 parts per activation
+  typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+  auto dot2 = [](uint32_t a, uint32_t b, float c) {
+    if constexpr (kH) return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+    else return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2_t, a), __builtin_bit_cast(bf2_t, b), c, false);
+  };
   // load the output pointer now (else its kernel-argument load sits between
   // the final reduction and the store)
   __asm__ volatile("" ::"s"(reinterpret_cast<uint64_t>(O)));
@@ -35,15 +48,32 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
   const int half_k = K >> 1;
 
   // 1. activations (k-permuted) for this lane's k-ranges
-  u32x4_t xv[M_][NSEG][4];
+  u32x4_t xv[M_][NSEG][NP][4];
 #pragma unroll
   for (int m = 0; m < M_; ++m)
 #pragma unroll
     for (int c = 0; c < NSEG; ++c) {
       const int k0 = min(c * 2048 + lane * 32, K - 32);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        xv[m][c][e] = *reinterpret_cast<const u32x4_t*>(X + size_t(m < M ? m : 0) * K + k0 + e * 8);
+      for (int e = 0; e < 4; ++e) {
+        const size_t at = size_t(m < M ? m : 0) * K + k0 + e * 8;
+        if constexpr (XD == LQ_F32) {
+          const float* xf = static_cast<const float*>(X) + at;
+          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xf);
+          const u32x4_t b = *reinterpret_cast<const u32x4_t*>(xf + 4);
+          const uint32_t x8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            uint32_t h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) h[i] = f32_part_bits(x8[i], p) >> 16;
+            xv[m][c][p][e] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                     h[6] | (h[7] << 16)};
+          }
+        } else {
+          xv[m][c][0][e] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(X) + at);
+        }
+      }
     }
   // 2. scales of (row, segment)
   const stype* sp = static_cast<const stype*>(S);
@@ -54,7 +84,11 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
     for (int c = 0; c < NSEG; ++c) {
       const int k0 = min(c * 2048 + lane * 32, K - 32);
       const int n = min(n0 + r, N - 1);
-      sv[r][c] = sp[size_t(n) * num_scales + k0 / group];
+      const size_t si = size_t(n) * num_scales + k0 / group;
+      if constexpr (SD == kRT)
+        sv[r][c] = load_scale<kRT>(static_cast<const uint8_t*>(S) + si * (sd_rt == LQ_F32 ? 4 : 2), sd_rt);
+      else
+        sv[r][c] = sp[si];
     }
   __builtin_amdgcn_sched_barrier(0);
   // 3. all weights of this wave
@@ -71,7 +105,7 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
   __builtin_amdgcn_sched_barrier(0);
 
   // 4. permute activations, bias correction per (m, segment)
-  const half2_t ones = {half_t(1.f), half_t(1.f)};
+  const uint32_t ones = kH ? 0x3C003C00u : 0x3F803F80u;   // (1, 1) as fp16 / bf16
   float corr[M_][NSEG];
 #pragma unroll
   for (int m = 0; m < M_; ++m)
@@ -79,16 +113,19 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
     for (int c = 0; c < NSEG; ++c) {
       float sum = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xv[m][c][e] = xperm8(xv[m][c][e]);
-        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].x), ones, sum, false);
-        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].y), ones, sum, false);
-        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].z), ones, sum, false);
-        sum = __builtin_amdgcn_fdot2(as_h2(xv[m][c][e].w), ones, sum, false);
-      }
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xv[m][c][p][e] = xperm8(xv[m][c][p][e]);
+          sum = dot2(xv[m][c][p][e].x, ones, sum);
+          sum = dot2(xv[m][c][p][e].y, ones, sum);
+          sum = dot2(xv[m][c][p][e].z, ones, sum);
+          sum = dot2(xv[m][c][p][e].w, ones, sum);
+        }
       const bool valid = (m < M) && (c * 2048 + lane * 32 < K);
-      corr[m][c] = valid ? sum * kInt4Bias : 0.f;
+      corr[m][c] = valid ? sum * (kH ? kInt4Bias : 136.0f) : 0.f;
     }
+  const uint32_t magic = opaque_u32(kH ? 0x64006400u : 0x43004300u);
 
   // 5. rows
   float acc[M_][RW];
@@ -104,20 +141,25 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
       float pe[M_][4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const u32x4_t b = int4x8_biased_kperm(wv[r][c][e]);
+        const u32x4_t b = int4x8_biased_kperm_m(wv[r][c][e], magic);
 #pragma unroll
         for (int m = 0; m < M_; ++m) {
-          float t = __builtin_amdgcn_fdot2(as_h2(b.x), as_h2(xv[m][c][e].x), 0.f, false);
-          t = __builtin_amdgcn_fdot2(as_h2(b.y), as_h2(xv[m][c][e].y), t, false);
-          t = __builtin_amdgcn_fdot2(as_h2(b.z), as_h2(xv[m][c][e].z), t, false);
-          pe[m][e] = __builtin_amdgcn_fdot2(as_h2(b.w), as_h2(xv[m][c][e].w), t, false);
+          float t = 0.f;
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            t = dot2(b.x, xv[m][c][p][e].x, t);
+            t = dot2(b.y, xv[m][c][p][e].y, t);
+            t = dot2(b.z, xv[m][c][p][e].z, t);
+            t = dot2(b.w, xv[m][c][p][e].w, t);
+          }
+          pe[m][e] = t;
         }
       }
       float part[M_];
 #pragma unroll
       for (int m = 0; m < M_; ++m) part[m] = (pe[m][0] + pe[m][1]) + (pe[m][2] + pe[m][3]);
       float sc;
-      if constexpr (SD == LQ_F32) sc = sv[r][c];
+      if constexpr (SD == LQ_F32 || SD == kRT) sc = sv[r][c];
       else if constexpr (SD == LQ_F16) sc = float(sv[r][c]);
       else sc = bf16_to_f32(sv[r][c]);
       sc = valid ? sc : 0.f;
@@ -171,11 +213,11 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
       const float other = __shfl_xor(v[0], 64 / RW, 64);
       if ((lane & lowmask) == lowmask && (row & 1) == 0 && m < M && n0 + row + 1 < N) {
         const float g = v[0];
-        store_f32<OD>(O, size_t(m) * (N >> 1) + ((n0 + row) >> 1), g / (1.0f + expf(-g)) * other);
+        store_out<OD>(O, size_t(m) * (N >> 1) + ((n0 + row) >> 1), g / (1.0f + expf(-g)) * other, od_rt);
       }
     } else {
       if ((lane & lowmask) == lowmask && m < M && n0 + row < N)
-        store_f32<OD>(O, size_t(m) * N + n0 + row, v[0]);
+        store_out<OD>(O, size_t(m) * N + n0 + row, v[0], od_rt);
     }
   }
 }

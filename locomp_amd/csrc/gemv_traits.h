@@ -95,15 +95,6 @@ __device__ __forceinline__ u32x2_t int8x4_bf16_biased(uint32_t w) {
   r.y = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
   return r;
 }
-// Part `part` (0 hi, 1 mid, 2 lo) of the exact 3-way bf16 split of fp32 x,
-// as the bf16 bit pattern in the high half of the returned dword.
-__device__ __forceinline__ uint32_t f32_part_bits(uint32_t x, int part) {
-  const uint32_t hi = x & 0xFFFF0000u;
-  const float r1 = __uint_as_float(x) - __uint_as_float(hi);
-  const uint32_t mid = __float_as_uint(r1) & 0xFFFF0000u;
-  const float r2 = r1 - __uint_as_float(mid);
-  return part == 0 ? hi : part == 1 ? mid : __float_as_uint(r2);
-}
 
 template <> struct TileMfma<4, LQ_BF16> {
   static constexpr int kSpan = 32;

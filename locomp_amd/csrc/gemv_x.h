@@ -122,6 +122,38 @@ static int launch_seg_x(const void* X, const void* W, const void* S, void* O, in
   return check_launch();
 }
 
+// The row kernel (int4, G % 32) with bf16 (M <= 2) or fp32 (M = 1, K <= 4096)
+// activations, scale / output dtypes at run time; segment counts and rows
+// per wave as for fp16.
+template <int M_, int XD>
+static int launch_rows_x_m(const void* X, const void* W, const void* S, void* O, int64_t M,
+                           int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  const int64_t nseg = (K + 2047) / 2048;
+  if (nseg <= 2 && N <= 3072) {
+    if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 1, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    return launch_gemv_rows_t<M_, 2, 1, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+  }
+  if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+  if (nseg <= 2)
+    return launch_gemv_rows_t<M_, 2, 4, kRT, kRT, false, (M_ == 2 || XD == LQ_F32) ? 2 : 3, XD>(
+        X, W, S, O, M, N, K, G, st, sd, od);
+  if constexpr (M_ == 1 && XD != LQ_F32) {
+    if (nseg == 3) return launch_gemv_rows_t<M_, 3, 2, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    if (nseg == 4) return launch_gemv_rows_t<M_, 4, 2, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    if (nseg <= 6) return launch_gemv_rows_t<M_, 6, 2, kRT, kRT, false, 2, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    return launch_gemv_rows_t<M_, 8, 2, kRT, kRT, false, 2, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+  }
+  return LQ_ERR_SHAPE;
+}
+
+static int launch_rows_x(const void* X, const void* W, const void* S, void* O, int64_t M,
+                         int64_t N, int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
+  if (M > (xd == LQ_F32 ? 1 : 2)) return LQ_ERR_SHAPE;
+  if (xd == LQ_F32) return launch_rows_x_m<1, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
+  if (M == 1) return launch_rows_x_m<1, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+  return launch_rows_x_m<2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+}
+
 // bf16 activations at M <= 16, fp32 at M <= 4 (three MFMA rows per
 // activation row), on the shapes gemv_tile_ok accepts; LQ_ERR_SHAPE otherwise.
 // int4 M = 1 with G % 128 takes the segment kernel.  fp32 activations are
@@ -137,6 +169,13 @@ int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_
   if constexpr (WBITS == 4) {
     const int rc = launch_seg_x(X, W, S, O, M, N, K, G, xd, sd, od, st);
     if (rc != LQ_ERR_SHAPE) return rc;
+    // the row kernel for what the segment kernel leaves at M <= 2 (fp32:
+    // M = 1, K <= 4096), as for fp16: rows the tile kernel does not take
+    // (SmolLM2 576 x 1536 G = 32: 6.8 -> 2.7 us bf16, 7.0 -> 3.7 fp32, on
+    // the generic kernel before) and faster than it where it does (4096 x
+    // 4096 G = 32: bf16 7.8 -> 5.6, M = 2 7.9 -> 6.9, fp32 9.8 -> 8.2)
+    if (M <= (xd == LQ_F32 ? 1 : 2) && gemv_rows_ok(4, M, K, G) && (xd != LQ_F32 || K <= 4096))
+      return launch_rows_x(X, W, S, O, M, N, K, G, xd, sd, od, st);
   }
   if (xd == LQ_F32 ? M > 4 : M > 16) return LQ_ERR_SHAPE;
   if (!gemv_tile_ok(WBITS, M, N, K, G, sd == LQ_F32 ? 4 : 2)) return LQ_ERR_SHAPE;

@@ -194,6 +194,16 @@ __device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
   return v;
 }
 
+// Part `part` (0 hi, 1 mid, 2 lo) of the exact 3-way bf16 split of fp32 x,
+// as the bf16 bit pattern in the high half of the returned dword.
+__device__ __forceinline__ uint32_t f32_part_bits(uint32_t x, int part) {
+  const uint32_t hi = x & 0xFFFF0000u;
+  const float r1 = __uint_as_float(x) - __uint_as_float(hi);
+  const uint32_t mid = __float_as_uint(r1) & 0xFFFF0000u;
+  const float r2 = r1 - __uint_as_float(mid);
+  return part == 0 ? hi : part == 1 ? mid : __float_as_uint(r2);
+}
+
 constexpr float kInt4Bias = 1032.0f;
 constexpr float kInt8Bias = 1152.0f;
 

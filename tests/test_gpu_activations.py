@@ -190,6 +190,31 @@ def test_fp32_activations_beyond_four_rows_low_precision_out(od):
     np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("xd", ["bf16", "f32"])
+@pytest.mark.parametrize("M,N,K,G,sd,od", [
+    (1, 576, 576, 32, "f16", "f16"),      # SmolLM2 shapes (the tile kernel's rows are too short)
+    (1, 576, 1536, 32, "bf16", "f32"),
+    (1, 3072, 576, 32, "f32", "bf16"),
+    (2, 960, 576, 32, "f16", "f32"),      # bf16 M = 2 (fp32 M = 2 takes the tile kernel)
+    (1, 2048, 2048, 64, "f16", "f16"),
+    (1, 300, 4032, 96, "f32", "f32"),     # 2 segments
+    (1, 1000, 6144, 32, "f16", "f16"),    # bf16: 3 segments (fp32 K > 4096: tile kernel)
+    (1, 257, 11008, 32, "f16", "f16"),    # bf16: 6 segments, partial
+    (2, 333, 3200, 64, "bf16", "bf16"),
+])
+def test_row_kernel_bf16_fp32_activations(xd, M, N, K, G, sd, od):
+    """The row kernel (M <= 2, G % 32) with bf16 / fp32 activations: bf16
+    weights 128 + q and v_dot2_f32_bf16, fp32 as three exact bf16 parts; fp32
+    outputs at rtol 1e-4, others at 1e-2."""
+    X, W, S = _case(4, M, N, K, G, seed=M + N + K + G)
+    got = _run(4, X, W, S, N, K, G, xd, sd, od)
+    want = _oracle(4, _used(X, xd), W, _used(S, sd), G)
+    if xd == "f32" and od == "f32":
+        _close32(got, want)
+    else:
+        np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+
+
 def test_fp32_split_is_exact_on_hard_values():
     """Activations with 24 significant bits, tiny and huge magnitudes: the
     three-part split must reproduce fp32 products (one weight row of ones,
