@@ -85,6 +85,9 @@ template <int WBITS>
 static int matmul_f32_stacked(const void* X, const void* W, const void* S, void* O, int64_t K,
                               int64_t G, int64_t N, int64_t M, int sd, int od, hipStream_t st) {
   if (3 * M > 16 && (G % 32 != 0 || K % 64 != 0)) return LQ_ERR_SHAPE;
+  // below ~2^24 multiply-adds its three launches cost more than the generic
+  // kernel (16 x 576 x 576: 20 us against 11)
+  if (M * N * K < (int64_t(1) << 24)) return LQ_ERR_SHAPE;
   constexpr int64_t kCap = int64_t(256) << 20;          // bytes per workspace slot
   const int64_t rows = std::max<int64_t>(1, std::min(kCap / (3 * K * 2), kCap / (3 * N * 4)));
   const int64_t mb = std::min(M, rows);

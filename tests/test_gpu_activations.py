@@ -162,14 +162,15 @@ def test_fp32_activations_shapes(wbits, M, N, K, G, sd):
 
 
 @pytest.mark.parametrize("wbits,M,N,K,G,sd", [
-    (4, 5, 300, 2048, 64, "f16"),       # 15 part rows: the tile kernel
-    (4, 6, 257, 4096, 128, "f32"),      # 18 part rows: the bf16 GEMM (split K)
-    (8, 16, 1000, 1024, 128, "bf16"),
+    (4, 5, 2000, 2048, 64, "f16"),      # 15 part rows: the tile kernel
+    (4, 6, 1000, 4096, 128, "f32"),     # 18 part rows: the bf16 GEMM (split K)
+    (8, 16, 1100, 1024, 128, "bf16"),
     (4, 64, 1000, 4096, 128, "f16"),
     (8, 300, 640, 2048, 256, "f32"),
     (4, 2048, 4096, 4096, 128, "f16"),  # BASELINE cfg 5a shape with fp32 activations
-    (4, 8, 256, 512, 32, "f16"),        # G = 32: the GEMM scales after each 32-k half
-    (8, 40, 300, 1152, 96, "f32"),      # G = 96: groups end mid-step and at step ends
+    (4, 8, 2048, 1024, 32, "f16"),      # G = 32: the GEMM scales after each 32-k half
+    (8, 40, 600, 1152, 96, "f32"),      # G = 96: groups end mid-step and at step ends
+    (4, 16, 576, 576, 32, "f16"),       # < 2^24 multiply-adds: the generic kernel
 ])
 def test_fp32_activations_beyond_four_rows(wbits, M, N, K, G, sd):
     """fp32 activations at M > 4: exact bf16 parts stacked as 3 M rows on the
@@ -302,7 +303,7 @@ def test_fp32_activations_beyond_four_rows_in_graph():
 
     lib = _lib.load()
     vp = ctypes.c_void_p
-    M, N, K, G = 8, 256, 512, 128
+    M, N, K, G = 8, 2048, 1024, 128
     X, W, S = _case(4, M, N, K, G, seed=78)
     want = _oracle(4, X, W, S, G)
     Xd, Wd, Sd = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (X, W, S))
