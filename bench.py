@@ -444,7 +444,7 @@ def main():
             run_case(f"gemv_w4a16_M{M}", Case("matvec", 4, M, c3["N"], c3["K"], c3["G"], c3["lo"],
                                                 c3["hi"]), "hbm")
     for xd in ("bf16", "f32"):
-        for M in ((1, 4, 16) if xd == "bf16" else (1, 4)):
+        for M in (1, 4, 16):
             if want(f"gemv_{xd}"):
                 run_case(f"gemv_w4a{xd}_M{M}", Case("matvec", 4, M, c3["N"], c3["K"], c3["G"],
                                                               c3["lo"], c3["hi"], xd=xd), "hbm")
@@ -453,6 +453,13 @@ def main():
         run_case("gemm_prefill_w4abf16_2048x4096x4096_g128",
                  Case("matvec", 4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
                       min_bytes=0, max_replicas=4, xd="bf16"), "mfma")
+    if want("gemm_prefill_f32"):
+        # fp32 activations (the reference's dtype): exact bf16 parts as 3 M
+        # rows on the bf16 GEMM, then the part rows added
+        c = synth.CFG5A
+        run_case("gemm_prefill_w4af32_2048x4096x4096_g128",
+                 Case("matvec", 4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
+                      min_bytes=0, max_replicas=4, xd="f32"), "mfma")
     if want("launch_floor"):
         # one 1 KB streaming read per launch: the per-launch cost of a graph
         # node on this part, which bounds a stack of small dependent launches
