@@ -27,6 +27,9 @@ template <int WBITS>
 int launch_gemm(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
                 int, int, hipStream_t, const FixedScratch*);
 template <int WBITS>
+int launch_tile_xl_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                     int64_t, int, int, hipStream_t);
+template <int WBITS>
 int launch_gemm_split_only(const void*, const void*, const void*, void*, int64_t, int64_t,
                            int64_t, int64_t, int, int, hipStream_t, const FixedScratch*);
 int launch_zero_fill(void*, int64_t, int, hipStream_t);
@@ -135,6 +138,14 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
   if (fast_common && xd == LQ_F32 && M > 4 && fixed == nullptr) {
     // fp32 beyond the decode kernels' 4 rows: exact bf16 parts on the bf16 route
     const int rc = matmul_f32_stacked<WBITS>(X, W, S, O, K, G, N, M, sd, od, st);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
+  if (fast_common && xd == LQ_BF16 && M > 16 && M <= 64 &&
+      !(N > 3072 && N <= 4096 && K >= 10240)) {
+    // bf16 decode / verify sizes: the activation-in-LDS kernel (bf16 MFMAs);
+    // few long rows (the split-GEMM shapes of the fp16 route) and other
+    // shapes it does not take go to the GEMM below
+    const int rc = launch_tile_xl_x<WBITS>(X, W, S, O, M, N, K, G, sd, od, st);
     if (rc != LQ_ERR_SHAPE) return rc;
   }
   if (fast_common && xd == LQ_BF16 && M > 16 && K % 64 == 0) {

@@ -331,15 +331,17 @@ static bool gemv_tile_xl_ok(int wbits, int64_t M, int64_t N, int64_t K, int64_t 
          (N * (K / G) * scale_bytes) % 4 == 0 &&
          gemv_tile_xl_count(wbits, N, K, G, scale_bytes, xl_mtiles(M)) > 0;
 }
-template <int WBITS, int SD, int OD, bool EPI, int MT>
+template <int WBITS, int SD, int OD, bool EPI, int MT, int XD = LQ_F16>
 static void launch_gemv_tile_xl_mt(const void* X, const void* W, const void* S, void* O, int64_t M,
-                                   int64_t N, int64_t K, int64_t G, hipStream_t st) {
-  const int tiles = gemv_tile_xl_count(WBITS, N, K, G, SD == LQ_F32 ? 4 : 2, MT);
+                                   int64_t N, int64_t K, int64_t G, hipStream_t st, int sd_rt = 0,
+                                   int od_rt = 0) {
+  const int ssz = (SD == kRT ? sd_rt : SD) == LQ_F32 ? 4 : 2;
+  const int tiles = gemv_tile_xl_count(WBITS, N, K, G, ssz, MT);
   const unsigned blocks = unsigned((N + 16 * tiles - 1) / (16 * tiles));
 #define LQ_TX(T_)                                                                              \
-  hipLaunchKernelGGL((gemv_tile_xl_kernel<WBITS, T_, SD, OD, EPI, MT>), dim3(blocks), dim3(512), 0, \
-                     st, static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O,  \
-                     int(M), int(N), int(K), int(K / G), int(G))
+  hipLaunchKernelGGL((gemv_tile_xl_kernel<WBITS, T_, SD, OD, EPI, MT, XD>), dim3(blocks), dim3(512), \
+                     0, st, X, static_cast<const uint8_t*>(W), S, O, int(M), int(N), int(K),   \
+                     int(K / G), int(G), sd_rt, od_rt)
   if constexpr (WBITS == 8) {
     switch (tiles) {
       case 1: LQ_TX(1); break;

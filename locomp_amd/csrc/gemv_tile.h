@@ -357,11 +357,14 @@ constexpr int xl_scale_bytes(int wbits, int tiles, int mtiles) {
 
 // EPI: gate/up rows interleaved; store silu(gate) * up to O [M, N / 2].
 // MT: 16-row activation tiles (2 for M <= 32, else 4).
-template <int WBITS, int TILES, int SD, int OD, bool EPI = false, int MT = 4>
+template <int WBITS, int TILES, int SD, int OD, bool EPI = false, int MT = 4, int XD = LQ_F16>
 __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
-    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
-    void* __restrict__ O, int M, int N, int K, int num_scales, int group) {
-  typedef TileMfma<WBITS> Mf;
+    const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
+    int od_rt = 0) {
+  static_assert(XD == LQ_F16 || XD == LQ_BF16, "fp16 or bf16 activations");
+  constexpr bool kH = XD == LQ_F16;
+  typedef TileMfma<WBITS, XD> Mf;
   typedef typename Mf::op_t op_t;
   const float rgroup = 1.0f / float(group);             // for div_rcp (K < 2^22)
   constexpr int kRows = 16 * TILES;
@@ -370,7 +373,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
   constexpr int kWBytes = kRows * kRowB;
   constexpr int kXBytes = 16 * MT * kXChunkK * 2;         // 16 MT activation rows, fp16
   constexpr int kSlotB = kWBytes + kXBytes;
-  constexpr int kSSize = SD == LQ_F32 ? 4 : 2;
+  const int kSSize = SD == kRT ? (sd_rt == LQ_F32 ? 4 : 2) : (SD == LQ_F32 ? 4 : 2);
   constexpr int kWInstr = kWBytes / 1024;
   constexpr int kInstr = kWInstr + kXBytes / 1024;
   constexpr int kPerWaveMax = (kInstr + 7) / 8;
@@ -413,7 +416,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     } else {
       const int row = 2 * (j - kWInstr) + (lane >> 5);
       const int m = min(row, M - 1);
-      src[i] = reinterpret_cast<const uint8_t*>(X + size_t(m) * K) + (((lane & 31) ^ (row & 15)) << 4);
+      src[i] = reinterpret_cast<const uint8_t*>(static_cast<const uint16_t*>(X) + size_t(m) * K) + (((lane & 31) ^ (row & 15)) << 4);
       dst[i] = kWBytes + (j - kWInstr) * 1024;
     }
   }
@@ -453,7 +456,7 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
       dma16_buf(rsrc, uint32_t(j * 1024 + lane * 16), &sl[j * 1024]);
   }
 
-  const uint32_t magic = opaque_u32(0x64006400u);
+  const uint32_t magic = opaque_u32(Mf::kMagic);
   float4_t acc[MT][TILES];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -472,7 +475,8 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     for (int t = 0; t < TILES; ++t) {
       const uint8_t* ps = sl + (size_t(t * 16 + r16) * num_scales + g) * kSSize;
       float sc;
-      if constexpr (SD == LQ_F32) sc = *reinterpret_cast<const float*>(ps);
+      if constexpr (SD == kRT) sc = load_scale<kRT>(ps, sd_rt);
+      else if constexpr (SD == LQ_F32) sc = *reinterpret_cast<const float*>(ps);
       else if constexpr (SD == LQ_F16) sc = float(*reinterpret_cast<const half_t*>(ps));
       else sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(ps));
 #pragma unroll
@@ -496,27 +500,38 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     if constexpr (WBITS == 8) {
       // one 16x16x32 block: the lane's 8 k are wave * 32 + q4 * 8 ..: bytes
       // 8 q4 of weight position 2 wave + q4 / 2, activation position 4 wave + q4;
-      // the int8 weights are converted to fp16 exactly.
-      h8 bw[TILES];
+      // the int8 weights are converted to fp16 (bf16 activations: bf16)
+      // exactly.
+      u32x4_t bw[TILES];
 #pragma unroll
       for (int t = 0; t < TILES; ++t) {
         const int row = t * 16 + r16;
         const u32x2_t w = *reinterpret_cast<const u32x2_t*>(
             wl + row * kRowB + (((2 * wave + (q4 >> 1)) ^ (row & (kPos - 1))) << 4) + ((q4 & 1) << 3));
-        half2_t lo[2], hi[2];
-        int8x4_to_h2(w.x, lo);
-        int8x4_to_h2(w.y, hi);
-        bw[t] = h8{lo[0][0], lo[0][1], lo[1][0], lo[1][1], hi[0][0], hi[0][1], hi[1][0], hi[1][1]};
+        if constexpr (kH) {
+          half2_t lo[2], hi[2];
+          int8x4_to_h2(w.x, lo);
+          int8x4_to_h2(w.y, hi);
+          bw[t] = u32x4_t{as_u32(lo[0]), as_u32(lo[1]), as_u32(hi[0]), as_u32(hi[1])};
+        } else {
+          const u32x2_t a = int8x4_to_bf16(w.x), b = int8x4_to_bf16(w.y);
+          bw[t] = u32x4_t{a.x, a.y, b.x, b.y};
+        }
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int row = mt * 16 + r16;
         const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(
             xl + row * (kXChunkK * 2) + (((4 * wave + q4) ^ (row & 15)) << 4));
-        const h8 xa = __builtin_bit_cast(h8, xv);
 #pragma unroll
-        for (int t = 0; t < TILES; ++t)
-          raw[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bw[t], raw[mt][t], 0, 0, 0);
+        for (int t = 0; t < TILES; ++t) {
+          if constexpr (kH)
+            raw[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(h8, xv), __builtin_bit_cast(h8, bw[t]), raw[mt][t], 0, 0, 0);
+          else
+            raw[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf8_t, xv), __builtin_bit_cast(bf8_t, bw[t]), raw[mt][t], 0, 0, 0);
+        }
       }
       if (--left == 0 || c + 1 == nchunks) {
         left = cpg;
@@ -584,9 +599,9 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
         const float g = v[r];
         const float up = __shfl_xor(g, 1, 64);
         if ((r16 & 1) == 0 && m < M && n < N)
-          store_f32<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up);
+          store_out<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up, od_rt);
       } else {
-        if (m < M && n < N) store_f32<OD>(O, size_t(m) * N + n, v[r]);
+        if (m < M && n < N) store_out<OD>(O, size_t(m) * N + n, v[r], od_rt);
       }
     }
   }

@@ -84,6 +84,16 @@ template <> struct TileMfma<8, LQ_F16> {
 __device__ __forceinline__ u32x4_t int4x8_bf16_biased(uint32_t w, uint32_t magic) {
   return int4x8_biased_kperm_m(w, magic);
 }
+// int8 -> four bf16 q, k order kept (exact: at most 8 significant bits, so
+// the float's low half is 0).
+__device__ __forceinline__ u32x2_t int8x4_to_bf16(uint32_t w) {
+  const float f0 = float(int8_t(w)), f1 = float(int8_t(w >> 8));
+  const float f2 = float(int8_t(w >> 16)), f3 = float(int8_t(w >> 24));
+  u32x2_t r;
+  r.x = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+  r.y = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+  return r;
+}
 // int8 -> four bf16 128 + q, k order kept (u = q ^ 0x80 = q + 128 is exact as
 // a float and as bf16: at most 8 significant bits, so the float's low half is 0).
 __device__ __forceinline__ u32x2_t int8x4_bf16_biased(uint32_t w) {

@@ -154,6 +154,23 @@ static int launch_rows_x(const void* X, const void* W, const void* S, void* O, i
   return launch_rows_x_m<2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
 }
 
+// bf16 activations at 16 < M <= 64 (int8 also 8 < M <= 16 with whole-chunk
+// groups, as for fp16) on the activation-in-LDS kernel with bf16 MFMAs;
+// LQ_ERR_SHAPE where it does not apply.
+template <int WBITS>
+int launch_tile_xl_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                     int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  if (!gemv_tile_xl_ok(WBITS, M, N, K, G, sd == LQ_F32 ? 4 : 2)) return LQ_ERR_SHAPE;
+  const int mt = xl_mtiles(M);
+  if (mt == 1 && WBITS == 8)
+    launch_gemv_tile_xl_mt<WBITS, kRT, kRT, false, 1, LQ_BF16>(X, W, S, O, M, N, K, G, st, sd, od);
+  else if (mt <= 2)
+    launch_gemv_tile_xl_mt<WBITS, kRT, kRT, false, 2, LQ_BF16>(X, W, S, O, M, N, K, G, st, sd, od);
+  else
+    launch_gemv_tile_xl_mt<WBITS, kRT, kRT, false, 4, LQ_BF16>(X, W, S, O, M, N, K, G, st, sd, od);
+  return check_launch();
+}
+
 // bf16 activations at M <= 16, fp32 at M <= 4 (three MFMA rows per
 // activation row), on the shapes gemv_tile_ok accepts; LQ_ERR_SHAPE otherwise.
 // int4 M = 1 with G % 128 takes the segment kernel.  fp32 activations are

@@ -20,6 +20,8 @@ int launch_sum_part_rows(const float* P, void* O, int64_t M, int64_t N, int od, 
   return check_launch();
 }
 
+template int launch_tile_xl_x<4>(const void*, const void*, const void*, void*, int64_t,
+                                  int64_t, int64_t, int64_t, int, int, hipStream_t);
 template int launch_skinny_x<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
                                 int64_t, int64_t, int, int, int, hipStream_t,
                                 const FixedScratch*);

@@ -87,6 +87,12 @@ def test_bf16_activations_cfg3(wbits, M):
     (8, 7, 333, 2064, 16),       # partial chunk, 16-k groups
     (8, 16, 130, 11008, 128),
     (8, 2, 64, 1536, 64),
+    (4, 33, 640, 2048, 64),      # 16 < M <= 64: the activation-in-LDS kernel, bf16 MFMAs
+    (4, 64, 1000, 4096, 128),
+    (4, 20, 11008, 1024, 32),
+    (8, 40, 300, 2048, 128),
+    (8, 24, 4100, 1536, 512),
+    (8, 64, 257, 1024, 1024),    # per channel: raw sums over the whole row
     (4, 1, 300, 6144, 128),      # segment kernel at 3 / 6 / 8 segments, 2 rows per wave
     (4, 1, 257, 11008, 128),
     (4, 1, 130, 14336, 256),
