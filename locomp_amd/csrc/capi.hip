@@ -34,6 +34,8 @@ int launch_gemm_split_only(const void*, const void*, const void*, void*, int64_t
                            int64_t, int64_t, int, int, hipStream_t, const FixedScratch*);
 int launch_zero_fill(void*, int64_t, int, hipStream_t);
 int launch_split_f32_rows(const float*, void*, int64_t, int64_t, hipStream_t);
+int launch_rows_silu_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                       int64_t, int, int, int, hipStream_t);
 int launch_sum_part_rows(const float*, void*, int64_t, int64_t, int, hipStream_t);
 int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
                     hipStream_t);
@@ -316,6 +318,10 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
       rc = launch_gemm_silu(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
     else if (fused)
       rc = launch_silu_fast(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
+    if (rc != LQ_ERR_SHAPE) return rc;
+    if (!fused && K_dim % 8 == 0)   // bf16 / fp32 activations or bf16 dtypes, M <= 2: the row kernel
+      rc = launch_rows_silu_x(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
+                              out_dtype, st);
     if (rc != LQ_ERR_SHAPE) return rc;
     // No fused kernel for this shape: the fast matvec into an fp32 staging
     // buffer (slot 1 of the stream's workspace), then the pairwise epilogue.

@@ -125,33 +125,48 @@ static int launch_seg_x(const void* X, const void* W, const void* S, void* O, in
 // The row kernel (int4, G % 32) with bf16 (M <= 2) or fp32 (M = 1, K <= 4096)
 // activations, scale / output dtypes at run time; segment counts and rows
 // per wave as for fp16.
-template <int M_, int XD>
+template <int M_, int XD, bool EPI = false>
 static int launch_rows_x_m(const void* X, const void* W, const void* S, void* O, int64_t M,
                            int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
   const int64_t nseg = (K + 2047) / 2048;
+  constexpr int kSmallRW = EPI ? 2 : 1;   // (gate / up pairs stay in one wave)
   if (nseg <= 2 && N <= 3072) {
-    if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 1, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
-    return launch_gemv_rows_t<M_, 2, 1, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    if (nseg <= 1) return launch_gemv_rows_t<M_, 1, kSmallRW, kRT, kRT, EPI, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    return launch_gemv_rows_t<M_, 2, kSmallRW, kRT, kRT, EPI, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
   }
-  if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+  if (nseg <= 1) return launch_gemv_rows_t<M_, 1, 4, kRT, kRT, EPI, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
   if (nseg <= 2)
-    return launch_gemv_rows_t<M_, 2, 4, kRT, kRT, false, (M_ == 2 || XD == LQ_F32) ? 2 : 3, XD>(
+    return launch_gemv_rows_t<M_, 2, 4, kRT, kRT, EPI, (M_ == 2 || XD == LQ_F32) ? 2 : 3, XD>(
         X, W, S, O, M, N, K, G, st, sd, od);
   if constexpr (M_ == 1 && XD != LQ_F32) {
-    if (nseg == 3) return launch_gemv_rows_t<M_, 3, 2, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
-    if (nseg == 4) return launch_gemv_rows_t<M_, 4, 2, kRT, kRT, false, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
-    if (nseg <= 6) return launch_gemv_rows_t<M_, 6, 2, kRT, kRT, false, 2, XD>(X, W, S, O, M, N, K, G, st, sd, od);
-    return launch_gemv_rows_t<M_, 8, 2, kRT, kRT, false, 2, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    if (nseg == 3) return launch_gemv_rows_t<M_, 3, 2, kRT, kRT, EPI, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    if (nseg == 4) return launch_gemv_rows_t<M_, 4, 2, kRT, kRT, EPI, 3, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    if (nseg <= 6) return launch_gemv_rows_t<M_, 6, 2, kRT, kRT, EPI, 2, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+    return launch_gemv_rows_t<M_, 8, 2, kRT, kRT, EPI, 2, XD>(X, W, S, O, M, N, K, G, st, sd, od);
   }
   return LQ_ERR_SHAPE;
 }
 
+// The row kernel with bf16 (M <= 2) or fp32 (M = 1, K <= 4096) activations
+// (fp16 too, for bf16 scales / outputs: then with kRT dtypes); EPI: the
+// gate / up SiLU * mul epilogue, O [M, N / 2].  LQ_ERR_SHAPE where it does
+// not apply.
+template <bool EPI = false>
 static int launch_rows_x(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
-  if (M > (xd == LQ_F32 ? 1 : 2)) return LQ_ERR_SHAPE;
-  if (xd == LQ_F32) return launch_rows_x_m<1, LQ_F32>(X, W, S, O, M, N, K, G, sd, od, st);
-  if (M == 1) return launch_rows_x_m<1, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
-  return launch_rows_x_m<2, LQ_BF16>(X, W, S, O, M, N, K, G, sd, od, st);
+  if (M > (xd == LQ_F32 ? 1 : 2) || !gemv_rows_ok(4, M, K, G) || (xd == LQ_F32 && K > 4096))
+    return LQ_ERR_SHAPE;
+  if (EPI && N % 2 != 0) return LQ_ERR_SHAPE;
+  if (xd == LQ_F32) return launch_rows_x_m<1, LQ_F32, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+  if (xd == LQ_BF16) {
+    if (M == 1) return launch_rows_x_m<1, LQ_BF16, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+    return launch_rows_x_m<2, LQ_BF16, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+  }
+  if constexpr (EPI) {
+    if (M == 1) return launch_rows_x_m<1, LQ_F16, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+    return launch_rows_x_m<2, LQ_F16, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+  }
+  return LQ_ERR_SHAPE;
 }
 
 // bf16 activations at 16 < M <= 64 (int8 also 8 < M <= 16 with whole-chunk
@@ -191,8 +206,8 @@ int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_
     // (SmolLM2 576 x 1536 G = 32: 6.8 -> 2.7 us bf16, 7.0 -> 3.7 fp32, on
     // the generic kernel before) and faster than it where it does (4096 x
     // 4096 G = 32: bf16 7.8 -> 5.6, M = 2 7.9 -> 6.9, fp32 9.8 -> 8.2)
-    if (M <= (xd == LQ_F32 ? 1 : 2) && gemv_rows_ok(4, M, K, G) && (xd != LQ_F32 || K <= 4096))
-      return launch_rows_x(X, W, S, O, M, N, K, G, xd, sd, od, st);
+    const int rr = launch_rows_x(X, W, S, O, M, N, K, G, xd, sd, od, st);
+    if (rr != LQ_ERR_SHAPE) return rr;
   }
   if (xd == LQ_F32 ? M > 4 : M > 16) return LQ_ERR_SHAPE;
   if (!gemv_tile_ok(WBITS, M, N, K, G, sd == LQ_F32 ? 4 : 2)) return LQ_ERR_SHAPE;

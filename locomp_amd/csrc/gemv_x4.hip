@@ -22,6 +22,14 @@ int launch_sum_part_rows(const float* P, void* O, int64_t M, int64_t N, int od, 
 
 template int launch_tile_xl_x<4>(const void*, const void*, const void*, void*, int64_t,
                                   int64_t, int64_t, int64_t, int, int, hipStream_t);
+// Gate / up rows interleaved with the SiLU * mul epilogue on the row kernel
+// for what the fp16 fused kernels do not take (bf16 / fp32 activations,
+// bf16 scales or outputs), M <= 2 (fp32: M = 1, K <= 4096).
+int launch_rows_silu_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                       int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
+  return launch_rows_x<true>(X, W, S, O, M, N, K, G, xd, sd, od, st);
+}
+
 template int launch_skinny_x<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
                                 int64_t, int64_t, int, int, int, hipStream_t,
                                 const FixedScratch*);

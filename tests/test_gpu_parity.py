@@ -569,7 +569,8 @@ def test_matvec_int4_silu_mul(policy, M, I, K, G, xd):
 
 
 @pytest.mark.parametrize("M,I,K,G", [(1, 1536, 576, 32), (4, 700, 2048, 128), (40, 300, 2048, 64),
-                                     (130, 256, 1024, 128)])
+                                     (130, 256, 1024, 128),
+                                     (2, 700, 1024, 32), (1, 3000, 4096, 64)])   # row kernel epilogue
 @pytest.mark.parametrize("xd,sd,od", [("f16", "bf16", "bf16"), ("bf16", "f16", "bf16"),
                                       ("bf16", "bf16", "f32"), ("f32", "f32", "f32")])
 def test_matvec_int4_silu_mul_other_dtypes(M, I, K, G, xd, sd, od):
