@@ -153,7 +153,7 @@ class Stack:
     (q, k, v, o, gate, up, down) at M = 1, random weights (BASELINE config 5b).
     One step = all 210 GEMVs of one token, launched back to back (in a graph)."""
 
-    def __init__(self, seed=0, G=32, fused=False, silu=False, chain=False):
+    def __init__(self, seed=0, G=32, fused=False, silu=False, chain=False, f32=False):
         """chain=True (with fused and silu) feeds every launch the previous
         one's output, in the order examples/54_smollm2_inference.py:494-554
         runs the linears: q|k|v -> o (on the q part, standing in for the
@@ -161,6 +161,9 @@ class Stack:
         layer's q|k|v.  Attention, norms and residual adds are not on the
         quantized path and are left out."""
         self.chain = chain and fused and silu
+        # f32=True: fp32 activations and outputs (the reference's tensor dtype)
+        self.dt = 0 if f32 else 1
+        adt = np.float32 if f32 else np.float16
         """fused=True concatenates the weights of linears that read the same
         activation (q|k|v: N = 960, gate|up: N = 3072): 4 GEMVs per layer.
         silu=True (with fused) runs gate|up as the fused SiLU * mul launch
@@ -174,7 +177,7 @@ class Stack:
         self.algo_bytes = 0
         xs = {}
         for K in (576, 1536):
-            xs[K] = _dev(synth.activations(rng, 1, K))
+            xs[K] = _dev(synth.activations(rng, 1, K, dtype=adt))
         self.xs = xs
         shapes = synth.SMOLLM2_LAYER
         if fused:
@@ -186,10 +189,11 @@ class Stack:
                 W = synth.int4_weights(rng, N, K)
                 S = synth.scales(rng, N, K // G, 0.001, 0.01)
                 epi = silu and fused and N == 2 * 1536
-                O = torch.empty(N // 2 if epi else N, dtype=torch.float16, device="cuda")
+                O = torch.empty(N // 2 if epi else N, dtype=torch.float32 if f32 else torch.float16,
+                                device="cuda")
                 x = prev if self.chain else self.xs[K]
                 self.layers.append((N, K, G, _dev(W), _dev(S), O, epi, x))
-                self.algo_bytes += W.nbytes + S.nbytes + K * 2 + (N // 2 if epi else N) * 2
+                self.algo_bytes += W.nbytes + S.nbytes + (K + (N // 2 if epi else N)) * (4 if f32 else 2)
                 prev = O     # (q|k|v: the o projection reads its first 576 = q)
         self.R = 1
         torch.cuda.synchronize()
@@ -200,11 +204,11 @@ class Stack:
             if epi:
                 rc = self.lib.locomp_amd_dequant_matvec_int4_silu_mul(
                     vp(x.data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
-                    K, K // 2, K // G, G, N // 2, 1, 1, 1, 1, stream)
+                    K, K // 2, K // G, G, N // 2, 1, self.dt, 1, self.dt, stream)
             else:
                 rc = self.lib.locomp_amd_dequant_matvec_int4(
                     vp(x.data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
-                    K, K // 2, K // G, G, N, 1, 1, 1, 1, stream)
+                    K, K // 2, K // G, G, N, 1, self.dt, 1, self.dt, stream)
             if rc != 0:
                 raise RuntimeError(f"launch failed: {rc}")
 
@@ -486,15 +490,17 @@ def main():
     if want("quantize"):
         run_case("quantize_int4_4096x4096_g32_from_f32", QuantCase(4096, 4096, 32), "hbm")
     if want("smollm2"):
-        for fused, silu, chain in ((False, False, False), (True, False, False), (True, True, False),
-                                   (True, True, True)):
-            st = Stack(fused=fused, silu=silu, chain=chain)
+        for fused, silu, chain, f32 in ((False, False, False, False), (True, False, False, False),
+                                        (True, True, False, False), (True, True, True, False),
+                                        (True, True, True, True)):
+            st = Stack(fused=fused, silu=silu, chain=chain, f32=f32)
             per, _ = time_graph(st, 4, 1)
             d = {"us_per_token": round(per * 1e6, 2), "GB_s": round(st.algo_bytes / per / 1e9, 1),
                  "gemvs_per_token": len(st.layers), "algorithmic_bytes": st.algo_bytes,
                  "us_per_gemv": round(per * 1e6 / len(st.layers), 3)}
             name = "smollm2_135m_int4_g32_decode_stack" + ("_qkv_gateup_fused" if fused else "") + \
-                ("_silu_epilogue" if silu else "") + ("_chained" if chain else "")
+                ("_silu_epilogue" if silu else "") + ("_chained" if chain else "") + \
+                ("_fp32_activations" if f32 else "")
             extra[name] = d
             log(name, d)
     if want("w8a16"):

@@ -23,9 +23,9 @@ namespace lq {
 // OCC: workgroups per CU the register budget is sized for (2 for 8 segments).
 // XD: activation dtype.  bf16 takes the weights decoded to bf16 128 + q
 // (0x4300 | q) and v_dot2_f32_bf16 (exact products, fp32 sums), the bias
-// 136 x the activation sum; fp32 takes three exact bf16 parts per activation
-// (hi + mid + lo), three dot products per weight pair.  SD / OD = kRT take
-// the scale / output dtypes from sd_rt / od_rt.
+// 136 x the activation sum; fp32 takes the nibbles as floats q (byte
+// conversions) in fp32 FMAs with the activations as loaded, the bias 8 x
+// their sum.  SD / OD = kRT take the scale / output dtypes from sd_rt / od_rt.
 template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3, int XD = LQ_F16>
 __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
     const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
@@ -33,7 +33,8 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
     int od_rt = 0) {
   typedef typename Elem<SD == kRT ? LQ_F32 : SD>::T stype;   // (kRT: converted at load)
   constexpr bool kH = XD == LQ_F16;
-  constexpr int NP = XD == LQ_F32 ? 3 : 1;      // bf16 parts per activation
+  constexpr bool kF = XD == LQ_F32;
+  constexpr int NP = kF ? 2 : 1;                // u32x4 per 8 activations
   typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
   auto dot2 = [](uint32_t a, uint32_t b, float c) {
     if constexpr (kH) return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
@@ -57,19 +58,10 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const size_t at = size_t(m < M ? m : 0) * K + k0 + e * 8;
-        if constexpr (XD == LQ_F32) {
+        if constexpr (kF) {
           const float* xf = static_cast<const float*>(X) + at;
-          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xf);
-          const u32x4_t b = *reinterpret_cast<const u32x4_t*>(xf + 4);
-          const uint32_t x8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            uint32_t h[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) h[i] = f32_part_bits(x8[i], p) >> 16;
-            xv[m][c][p][e] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                                     h[6] | (h[7] << 16)};
-          }
+          xv[m][c][0][e] = *reinterpret_cast<const u32x4_t*>(xf);
+          xv[m][c][1][e] = *reinterpret_cast<const u32x4_t*>(xf + 4);
         } else {
           xv[m][c][0][e] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(X) + at);
         }
@@ -112,18 +104,26 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
 #pragma unroll
     for (int c = 0; c < NSEG; ++c) {
       float sum = 0.f;
+      if constexpr (kF) {
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const u32x4_t v = xv[m][c][h][e];
+            sum += (__uint_as_float(v.x) + __uint_as_float(v.y)) + (__uint_as_float(v.z) + __uint_as_float(v.w));
+          }
+      } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          xv[m][c][p][e] = xperm8(xv[m][c][p][e]);
-          sum = dot2(xv[m][c][p][e].x, ones, sum);
-          sum = dot2(xv[m][c][p][e].y, ones, sum);
-          sum = dot2(xv[m][c][p][e].z, ones, sum);
-          sum = dot2(xv[m][c][p][e].w, ones, sum);
+          xv[m][c][0][e] = xperm8(xv[m][c][0][e]);
+          sum = dot2(xv[m][c][0][e].x, ones, sum);
+          sum = dot2(xv[m][c][0][e].y, ones, sum);
+          sum = dot2(xv[m][c][0][e].z, ones, sum);
+          sum = dot2(xv[m][c][0][e].w, ones, sum);
         }
+      }
       const bool valid = (m < M) && (c * 2048 + lane * 32 < K);
-      corr[m][c] = valid ? sum * (kH ? kInt4Bias : 136.0f) : 0.f;
+      corr[m][c] = valid ? sum * (kF ? 8.0f : kH ? kInt4Bias : 136.0f) : 0.f;
     }
   const uint32_t magic = opaque_u32(kH ? 0x64006400u : 0x43004300u);
 
@@ -141,18 +141,34 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
       float pe[M_][4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const u32x4_t b = int4x8_biased_kperm_m(wv[r][c][e], magic);
+        if constexpr (kF) {
+          // byte j of lo / hi = nibble 2j / 2j + 1 of the dword = k 8e + 2j (+ 1)
+          const uint32_t w = wv[r][c][e];
+          const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+          const float q[8] = {float(lo & 0xFFu), float(hi & 0xFFu), float((lo >> 8) & 0xFFu),
+                              float((hi >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
+                              float((hi >> 16) & 0xFFu), float(lo >> 24), float(hi >> 24)};
 #pragma unroll
-        for (int m = 0; m < M_; ++m) {
-          float t = 0.f;
-#pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            t = dot2(b.x, xv[m][c][p][e].x, t);
-            t = dot2(b.y, xv[m][c][p][e].y, t);
-            t = dot2(b.z, xv[m][c][p][e].z, t);
-            t = dot2(b.w, xv[m][c][p][e].w, t);
+          for (int m = 0; m < M_; ++m) {
+            const u32x4_t a0 = xv[m][c][0][e], a1 = xv[m][c][1][e];
+            float t = q[0] * __uint_as_float(a0.x);
+            t = fmaf(q[1], __uint_as_float(a0.y), t);
+            t = fmaf(q[2], __uint_as_float(a0.z), t);
+            t = fmaf(q[3], __uint_as_float(a0.w), t);
+            t = fmaf(q[4], __uint_as_float(a1.x), t);
+            t = fmaf(q[5], __uint_as_float(a1.y), t);
+            t = fmaf(q[6], __uint_as_float(a1.z), t);
+            pe[m][e] = fmaf(q[7], __uint_as_float(a1.w), t);
           }
-          pe[m][e] = t;
+        } else {
+          const u32x4_t b = int4x8_biased_kperm_m(wv[r][c][e], magic);
+#pragma unroll
+          for (int m = 0; m < M_; ++m) {
+            float t = dot2(b.x, xv[m][c][0][e].x, 0.f);
+            t = dot2(b.y, xv[m][c][0][e].y, t);
+            t = dot2(b.z, xv[m][c][0][e].z, t);
+            pe[m][e] = dot2(b.w, xv[m][c][0][e].w, t);
+          }
         }
       }
       float part[M_];
