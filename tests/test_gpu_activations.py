@@ -238,6 +238,23 @@ def test_fp32_split_is_exact_on_hard_values():
     assert np.abs(got - want).max() <= 2e-5 * scale
 
 
+@pytest.mark.parametrize("K", [576, 2048, 4096])
+def test_fp32_row_kernel_on_hard_values(K):
+    """The row kernel's fp32 path (int4, G = 32: fp32 FMAs on the nibbles as
+    floats) on activations spread over 2^40: every weight is q - 8 = 1, so
+    Y = sum(x), known in float64; the error must stay at fp32-accumulation
+    size, far below one bf16 rounding of the largest terms."""
+    rng = np.random.default_rng(6)
+    N, G = 48, 32
+    X = (rng.standard_normal((1, K)) * np.exp2(rng.integers(-20, 20, (1, K)))).astype(np.float32)
+    W = np.full((N, K // 2), 0x99, np.uint8)
+    S = np.ones((N, K // G), np.float32)
+    got = _run(4, X, W, S, N, K, G, "f32", "f32", "f32")
+    want = np.full((1, N), X.astype(np.float64).sum(), np.float64)
+    scale = np.abs(X.astype(np.float64)).sum()
+    assert np.abs(got - want).max() <= 2e-5 * scale
+
+
 def test_fp32_split_is_exact_on_hard_values_m3():
     """The same at M = 3 (the rows are split into bf16 part rows by a separate
     kernel first): row m of X scaled by 2^m, one weight row of ones."""
