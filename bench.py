@@ -457,6 +457,12 @@ def main():
         run_case("gemm_prefill_w4abf16_2048x4096x4096_g128",
                  Case("matvec", 4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
                       min_bytes=0, max_replicas=4, xd="bf16"), "mfma")
+    if want("cfg1"):
+        # BASELINE cfg 1, the reference's CPU-runnable case: W8A32, X fp32
+        # [4, 512], int8 [512, 512], per-channel fp32 scales, fp32 output
+        c = synth.CFG1
+        run_case("w8a32_M4_512x512_cfg1",
+                 Case("matvec", 8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"], xd="f32"), "hbm")
     if want("gemm_prefill_f32"):
         # fp32 activations (the reference's dtype): exact bf16 parts as 3 M
         # rows on the bf16 GEMM, then the part rows added

@@ -220,7 +220,9 @@ int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_
     default: launch_tile_x_nsc<WBITS, XD_, 4>(X, W, S, O, M, N, K, G, sd, od, st); break;   \
   }
   void* parts = nullptr;
-  if (xd == LQ_F32) {
+  // (small matrices: the tile kernel splits the activations itself, one
+  // launch instead of two; its smaller tile count costs nothing there)
+  if (xd == LQ_F32 && N * K >= (int64_t(1) << 22)) {
     const size_t bytes = size_t(12) * size_t(K) * 2;
     parts = fixed ? (bytes <= fixed->bytes ? fixed->p : nullptr) : stream_workspace(2, bytes, st);
   }
