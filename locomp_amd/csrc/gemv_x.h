@@ -154,6 +154,13 @@ static int launch_rows_x_m(const void* X, const void* W, const void* S, void* O,
 template <bool EPI = false>
 static int launch_rows_x(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, int xd, int sd, int od, hipStream_t st) {
+  // bf16 3 <= M <= 4 on one segment (K <= 2048) where the tile kernel does
+  // not apply (short rows: SmolLM2 at batch 4), four activation rows per
+  // lane: 576 x 576 4.2 -> 3.9 us against the generic kernel (fp32 lost
+  // there, 4.1 -> 4.9, and keeps the generic kernel)
+  if (xd == LQ_BF16 && M >= 3 && M <= 4 && K <= 2048 && K % 32 == 0 && G % 32 == 0 && !EPI &&
+      !gemv_tile_ok(4, M, N, K, G, sd == LQ_F32 ? 4 : 2))
+    return launch_gemv_rows_t<4, 1, 1, kRT, kRT, false, 2, LQ_BF16>(X, W, S, O, M, N, K, G, st, sd, od);
   if (M > (xd == LQ_F32 ? 1 : 2) || !gemv_rows_ok(4, M, K, G) || (xd == LQ_F32 && K > 4096))
     return LQ_ERR_SHAPE;
   if (EPI && N % 2 != 0) return LQ_ERR_SHAPE;

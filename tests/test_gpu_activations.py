@@ -208,6 +208,8 @@ def test_fp32_activations_beyond_four_rows_low_precision_out(od):
     (1, 1000, 6144, 32, "f16", "f16"),    # bf16: 3 segments (fp32 K > 4096: tile kernel)
     (1, 257, 11008, 32, "f16", "f16"),    # bf16: 6 segments, partial
     (2, 333, 3200, 64, "bf16", "bf16"),
+    (4, 576, 576, 32, "f16", "f32"),      # M = 3, 4 on short rows: four activation rows per lane
+    (3, 1536, 1536, 64, "bf16", "f16"),
 ])
 def test_row_kernel_bf16_fp32_activations(xd, M, N, K, G, sd, od):
     """The row kernel (M <= 2, G % 32) with bf16 / fp32 activations: bf16
