@@ -128,8 +128,9 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * M <= 2 with G % 32: bf16 dot products); fp32 at M <= 4 runs on bf16
  * matrix cores as three exact bf16 parts (split once per call into a
  * workspace, or inside the kernel on a capturing stream that has none yet
- * and on small matrices), except M = 1 with G % 128 != 0 and K <= 4096,
- * which takes fp32 FMAs on the row kernel;
+ * and on small matrices), except M = 1 with K <= 4096 where the segment
+ * kernel does not apply (K < 2048 or G % 128 != 0), which takes fp32 FMAs
+ * on the row kernel;
  * fp32 at M > 4 is split the same way into 3 M bf16 rows that take the bf16
  * route (3 M <= 16: the decode kernel; else the MFMA GEMM, G % 32 == 0)
  * with fp32 products, whose three part rows are then added; other fp32
