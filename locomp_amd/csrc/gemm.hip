@@ -88,6 +88,38 @@ constexpr int kAStages = 3;   // activation ring: steps ks, ks + 1, ks + 2
 constexpr int kGemmScaleFloats = 8192;   // int8 post-scale: BN x (K / G) fp32 scales
 constexpr int kBStages = 2;
 
+// XCD-aware tile order: workgroup b runs on XCD b % 8.  When the tile grid
+// splits into 8 equal blocks of gm x gn tiles, XCD x takes block x, with gm
+// chosen to minimise the bytes one k-step of the block reads (gm tiles of
+// `a_bytes` activation bytes per k + gn tiles of `b_bytes` weight bytes per
+// k): the XCD's L2 then holds the activation rows and weight rows its tiles
+// share.  Otherwise XCD x takes the contiguous slice [x per, (x + 1) per) of
+// the row-major tile list.  Returns the tile's row and column indices.
+__device__ __forceinline__ void xcd_tile(int b, int tiles_m, int tiles_n, int a_bytes, int b_bytes,
+                                         int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  int t = b, gm = 0;
+  if (total % 8 == 0) {
+    const int per = total >> 3;
+    int best = 1 << 30;
+    for (int d = 1; d <= tiles_m && d <= per; ++d) {
+      if (tiles_m % d || per % d || tiles_n % (per / d)) continue;
+      const int cost = d * a_bytes + (per / d) * b_bytes;
+      if (cost < best) { best = cost; gm = d; }
+    }
+    if (gm == 0) t = (b & 7) * per + (b >> 3);
+  }
+  if (gm > 0) {
+    const int gn = (total >> 3) / gm, gcols = tiles_n / gn;
+    const int xcd = b & 7, local = b >> 3;
+    tm = (xcd / gcols) * gm + local % gm;
+    tn = (xcd % gcols) * gn + local / gm;
+  } else {
+    tm = t / tiles_n;
+    tn = t % tiles_n;
+  }
+}
+
 // EPI: gate/up rows interleaved (2i, 2i + 1); store silu(gate) * up to
 // O [M, N / 2] (columns n and n + 1 sit in lanes r16 and r16 ^ 1).
 // XD: activation dtype, fp16 (fp16 MFMA) or bf16 (bf16 MFMA; B holds the
@@ -120,39 +152,10 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   const int wm = wave / C::WN;
   const int wn = wave % C::WN;
 
-  // XCD-aware tile order: workgroup b runs on XCD b % 8; XCD x takes the
-  // contiguous slice [x * per, (x + 1) * per) of the row-major tile list.
-  // XCD-aware tile order: workgroup b runs on XCD b % 8.  When the tile grid
-  // splits into 8 equal blocks of gm x gn tiles, XCD x takes block x, with
-  // gm chosen to minimise the bytes one k-step of the block reads (gm BM
-  // activation rows + gn BN weight rows): the XCD's L2 then holds the
-  // activation rows and weight rows its tiles share (cfg 5a: 4 x 8 tiles).
-  // Otherwise XCD x takes the contiguous slice [x per, (x + 1) per) of the
-  // row-major tile list.
-  const int total = tiles_m * tiles_n;
   int m0, n0;
-  {
-    int t = blockIdx.x, gm = 0;
-    if (total % 8 == 0) {
-      const int per = total >> 3;
-      int best = 1 << 30;
-      for (int d = 1; d <= tiles_m && d <= per; ++d) {
-        if (tiles_m % d || per % d || tiles_n % (per / d)) continue;
-        const int cost = d * BM * 2 + (per / d) * BN * WBITS / 8;
-        if (cost < best) { best = cost; gm = d; }
-      }
-      if (gm == 0) t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    }
-    if (gm > 0) {
-      const int gn = (total >> 3) / gm, gcols = tiles_n / gn;
-      const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
-      m0 = ((xcd / gcols) * gm + local % gm) * BM;
-      n0 = ((xcd % gcols) * gn + local / gm) * BN;
-    } else {
-      m0 = (t / tiles_n) * BM;
-      n0 = (t % tiles_n) * BN;
-    }
-  }
+  xcd_tile(blockIdx.x, tiles_m, tiles_n, BM * 2, BN * WBITS / 8, m0, n0);
+  m0 *= BM;
+  n0 *= BN;
   const int row_bytes = WBITS == 4 ? (K >> 1) : K;
   // split-K: workgroup row blockIdx.y covers k in [kbeg, min(kbeg + kspan, K))
   // (kspan a whole number of 64-k steps) and writes its fp32 partial sums to
@@ -491,6 +494,423 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   }
 }
 
+// ------------------------------------------------- pair-split int4 GEMM --
+// Prefill with int4 weights and fp16 activations on 128 x 256 output tiles
+// (cfg 5a: 16 x 16 tiles, one per CU).  Against the 256 x 128 kernel above it
+// moves a third fewer bytes from L2 per k (the int4 weight tile is the cheap
+// operand, so the tile is made wide in N) and about half the LDS bytes:
+//   * Waves (cb = w & 3, p = w >> 2): wave w owns output columns cb*64..+64 of
+//     the tile and all 128 rows (8 x 4 tiles of v_mfma_f32_16x16x32_f16, fp32
+//     accumulators in VGPRs), and of every 128-k unit only the 64-k stage p.
+//     The two waves of a column block (one SIMD each, if the hardware deals
+//     waves to SIMDs in turn) therefore split K, and add their sums through
+//     LDS once at the end.
+//   * Weights never pass through LDS: each wave loads its own packed bytes
+//     (lane (r16, q4) of column tile j: the 8 bytes of k = 16 q4 .. 16 q4 + 15
+//     of its stage, one 8-byte load) two units ahead into registers and
+//     dequantises them to exact fp16 (q - 8) * s just before its MFMAs.  Every
+//     weight of the tile is decoded once per workgroup.  The MFMA's k order
+//     inside the stage is permuted to match: block t of lane (r16, q4) holds
+//     k = 16 q4 + 8 t + i, i.e. 16-byte activation chunk 2 q4 + t of the row.
+//   * Activations: each unit's 128 x 128 fp16 tile is copied global -> LDS by
+//     direct-to-LDS buffer loads (XOR-swizzled chunks, as above) into a ring of
+//     four units (128 KB), three units ahead.  One barrier per unit.
+//   * Every wait is a hand-placed vmcnt that is exact under in-order
+//     completion: per unit each wave issues 4 weight loads, 4 scale loads and
+//     4 activation copies, in that order.
+// Needs K % 128 == 0 and a power-of-two group G >= 16 dividing K (a lane's 16
+// k then share one scale); the buffer sizes of X, W and the scales below 4 GB.
+constexpr int kPBM = 128, kPBN = 256, kPUnit = 128, kPLds = 160 * 1024;
+
+__device__ __forceinline__ u32x2_t bload_b64(i32x4_t rsrc, uint32_t voff, uint32_t soff) {
+  u32x2_t v;
+  __asm__ volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rsrc), "s"(soff) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t bload_u16(i32x4_t rsrc, uint32_t voff) {
+  uint32_t v;
+  __asm__ volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t bload_b32(i32x4_t rsrc, uint32_t voff) {
+  uint32_t v;
+  __asm__ volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t bload_u16_so(i32x4_t rsrc, uint32_t voff, uint32_t soff) {
+  uint32_t v;
+  __asm__ volatile("buffer_load_ushort %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rsrc), "s"(soff) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t bload_b32_so(i32x4_t rsrc, uint32_t voff, uint32_t soff) {
+  uint32_t v;
+  __asm__ volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rsrc), "s"(soff) : "memory");
+  return v;
+}
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4_t{int(uint32_t(a)), int(uint32_t(a >> 32) & 0xFFFFu), int(bytes), 0x00020000};
+}
+
+// Scheduling pattern for one row tile's 4 MFMAs and the work meant to run
+// under them: DS LDS reads after the first MFMA, VALU VALU ops after each.
+template <int DS, int VALU>
+__device__ __forceinline__ void interleave_mfma4() {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+    if constexpr (DS > 0)
+      if (j == 0) __builtin_amdgcn_sched_group_barrier(0x100, DS, 0);   // LDS read
+    __builtin_amdgcn_sched_group_barrier(0x002, VALU, 0);   // VALU
+  }
+}
+
+template <int SD, int OD, bool EPI, int SLOTS>
+__global__ __launch_bounds__(512, 1) void gemm_w4p_kernel(
+    const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int lg_group, int tiles_m,
+    int tiles_n) {
+  // SLOTS units of activations (32 KB each), then the tile's scale rows; the
+  // first 128 KB take the final reduction.
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kPLds];
+  half_t (*As)[kPBM * kBK] = reinterpret_cast<half_t (*)[kPBM * kBK]>(lds);
+  uint8_t* Ss = lds + SLOTS * 32768;
+  constexpr int kDA = SLOTS - 1;                 // activation copies run kDA units ahead
+  typedef typename Elem<SD>::T stype;
+  constexpr uint32_t kEs = sizeof(stype);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cb = wave & 3, p = wave >> 2;
+  const int r16 = lane & 15, q4 = lane >> 4;
+  int m0, n0;
+  xcd_tile(blockIdx.x, tiles_m, tiles_n, kPBM * 2, kPBN / 2, m0, n0);
+  m0 *= kPBM;
+  n0 *= kPBN;
+  const int units = K / kPUnit;
+  const uint32_t row_bytes = uint32_t(K) >> 1;
+
+  // A copies: wave w writes rows (w & 3) * 32 .. + 32 of stage p of a unit,
+  // 8 rows (1 KB) per instruction; lane L of instruction i: row 8 i + L / 8,
+  // chunk position L % 8 holding logical chunk (L % 8) ^ (row & 7).  Rows past
+  // M re-read row M - 1.
+  const i32x4_t xrsrc = buffer_rsrc(X, uint32_t(M) * uint32_t(K) * 2u);
+  const int arow = cb * 32 + (lane >> 3);        // row of copy 0; copy i adds 8 i
+  // LDS position x of a row holds logical chunk 2 (y & 3) + (y >> 2), y =
+  // x ^ (row & 7): the fragment of lane (r16, q4), block t (logical chunk
+  // 2 q4 + t) then sits at position (q4 + 4 t) ^ (row & 7), the positions of
+  // the 256 x 128 kernel's reads, which measured free of bank conflicts.
+  const int apos = (lane & 7) ^ (arow & 7);      // (row & 7: the same for every copy i)
+  const uint32_t achunk = uint32_t((2 * (apos & 3) + (apos >> 2)) * 16);
+  const uint32_t aoff0 = uint32_t(min(m0 + arow, M - 1)) * uint32_t(K) * 2u + achunk;
+  const uint32_t as_base = lds_addr(&As[0][0]) + uint32_t((p * kPBM * kBK + cb * 32 * kBK) * 2);
+
+  // Weight and scale rows of this lane's four column tiles (rows past N
+  // re-read row N - 1).
+  const i32x4_t wrsrc = buffer_rsrc(W, uint32_t(N) * row_bytes);
+  const uint32_t srow_bytes = uint32_t(num_scales) * kEs;
+  const i32x4_t srsrc = buffer_rsrc(S, uint32_t(N) * srow_bytes);
+  const int nb = n0 + cb * 64 + r16;             // row of column tile 0
+  const uint32_t bv0 = uint32_t(min(nb, N - 1)) * row_bytes + uint32_t(q4 * 8);
+
+  struct PSet {
+    u32x2_t b[4];     // packed weights: .x block t = 0, .y block t = 1
+  };
+  auto tie = [&](PSet& r) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) __asm__ volatile("" : "+v"(r.b[j]));
+  };
+  // The tile's scale rows are one contiguous block of 256 x num_scales
+  // entries; it is copied to LDS once (16 bytes per lane; rows past N read as
+  // 0), before every other load.
+  {
+    const uint32_t sbytes = uint32_t(kPBN) * srow_bytes;
+    const uint32_t sbase = uint32_t(n0) * srow_bytes;
+    const uint32_t ss_lds = lds_addr(&Ss[0]) + uint32_t(wave * 1024);
+    for (uint32_t o = 0; o < sbytes; o += 8192u)
+      dma16_so(srsrc, sbase + o + uint32_t(tid * 16), 0u, ss_lds + o);
+  }
+  const int srow0 = cb * 64 + r16;               // tile-local scale row of column tile 0
+
+  float4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t magic = opaque_u32(0x64006400u);
+  // exact fp16 (q - 8) * s of block t of column tile j
+  // scale of column tile j for unit u, as fp16
+  auto scale = [&](int j, int u) {
+    const int g = (u * kPUnit + p * 64 + q4 * 16) >> lg_group;
+    const stype v = *reinterpret_cast<const stype*>(&Ss[((srow0 + j * 16) * num_scales + g) * int(kEs)]);
+    if constexpr (SD == LQ_F16) return v;
+    else if constexpr (SD == LQ_F32) return half_t(v);
+    else return half_t(bf16_to_f32(v));
+  };
+  // exact fp16 (q - 8) * s of weights 2 e, 2 e + 1 of block t of column
+  // tile j: one half2 (4 VALU ops)
+  auto decode_pair = [&](const PSet& r, int j, int t, int e, half_t hs) {
+    const uint32_t w = t == 0 ? r.b[j].x : r.b[j].y;
+    const half2_t s2 = {hs, hs};
+    return as_u32(int4_pair_to_h2(w, e, magic) * s2);
+  };
+  auto read_a = [&](const half_t* a, int i, int t) {
+    const int m = i * 16 + r16;
+    return *reinterpret_cast<const h8*>(a + m * kBK + (((q4 + 4 * t) ^ (m & 7)) << 3));
+  };
+  // The main loop, for a tile whose rows and columns all exist (FULL: every
+  // row offset is a scalar step from the lane's first) or one at the matrix
+  // edge (rows clamped lane by lane).
+  auto main_loop = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    // copy i (8 rows, 1 KB) of this wave's share of unit ud's activations
+    auto dma = [&](int ud, int i) {
+      const uint32_t kd = uint32_t(min(ud, units - 1) * kPUnit + p * 64) * 2u;
+      const uint32_t slot = as_base + uint32_t((ud % SLOTS) * 2 * kPBM * kBK * 2 + i * 8 * kBK * 2);
+      if constexpr (FULL)
+        dma16_so(xrsrc, aoff0, kd + uint32_t(i * 8) * uint32_t(K) * 2u, slot);
+      else
+        dma16_so(xrsrc, uint32_t(min(m0 + arow + 8 * i, M - 1)) * uint32_t(K) * 2u + achunk, kd, slot);
+    };
+    auto bload = [&](PSet& r, int u, int j) {
+      const uint32_t kb = uint32_t(min(u, units - 1) * 64 + p * 32);
+      if constexpr (FULL) r.b[j] = bload_b64(wrsrc, bv0, kb + uint32_t(j * 16) * row_bytes);
+      else r.b[j] = bload_b64(wrsrc, uint32_t(min(nb + 16 * j, N - 1)) * row_bytes + uint32_t(q4 * 8), kb);
+    };
+    // Weights of unit u, then the activation copy of unit ud into its ring
+    // slot (units past the end re-read the last unit into slots no one reads
+    // again).
+    auto issue = [&](PSet& r, int u, int ud) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bload(r, u, j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dma(ud, i);
+    };
+    // Per unit each wave issues 4 weight loads (during the first 32-k block)
+    // then 4 activation copies (during the second), and every wait below is
+    // exact under in-order completion:
+    //  * top of unit u: the copy of unit u has landed: after it come the
+    //    kDA - 1 later units' 8 loads (units 0 and 1 with kDA = 3: the 12 loads
+    //    of the prologue's tail);
+    //  * middle of unit u: the weights of unit u + 1 have landed: after them
+    //    come one copy (4) and unit u's weight loads (4) (at unit 0 this also
+    //    waits for a prologue copy).
+    // After the barrier every wave's copy of unit u is in LDS and no wave
+    // still reads unit u - 1, whose slot then takes unit u + kDA.  Unit u's
+    // first 32-k block is decoded (into fb) during unit u - 1.  The loads are
+    // spread over the MFMAs, one per row tile: issued all at once, the 8
+    // waves' 64 loads queue in the CU's memory pipeline and stall the waves'
+    // issue (in-kernel timestamps: a quarter of the loop).
+    u32x4_t fb[4];
+    auto unit = [&](int u, PSet& cur, PSet& nxt, PSet& fut) {
+      if (kDA == 3 && u < 2) __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory");
+      else if constexpr (kDA == 3) __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      else __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      __syncthreads();
+      const half_t* a = As[(u % SLOTS) * 2 + p];
+      h8 fa[8];
+      u32x4_t fc[4];
+      half_t hs[4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) fa[i] = read_a(a, i, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hs[j] = scale(j, u);
+      __builtin_amdgcn_sched_barrier(0);
+      // block t = 0; under row tile i: its t = 1 fragment, two pairs of the
+      // t = 1 weights of column tile i / 2, and one load
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], __builtin_bit_cast(h8, fb[j]),
+                                                             acc[i][j], 0, 0, 0);
+        fa[i] = read_a(a, i, 1);
+        const int jj = i >> 1, e0 = (i & 1) * 2;
+        fc[jj][e0] = decode_pair(cur, jj, 1, e0, hs[jj]);
+        fc[jj][e0 + 1] = decode_pair(cur, jj, 1, e0 + 1, hs[jj]);
+        interleave_mfma4<1, 2>();
+        if (i < 4) bload(fut, u + 2, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      tie(nxt);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hs[j] = scale(j, u + 1 < units ? u + 1 : u);
+      __builtin_amdgcn_sched_barrier(0);
+      // block t = 1; under row tile i: two pairs of unit u + 1's t = 0
+      // weights of column tile i / 2
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], __builtin_bit_cast(h8, fc[j]),
+                                                             acc[i][j], 0, 0, 0);
+        const int jj = i >> 1, e0 = (i & 1) * 2;
+        fb[jj][e0] = decode_pair(nxt, jj, 0, e0, hs[jj]);
+        fb[jj][e0 + 1] = decode_pair(nxt, jj, 0, e0 + 1, hs[jj]);
+        interleave_mfma4<0, 2>();
+        if (i < 4) dma(u + kDA, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    PSet r0, r1, r2;
+    issue(r0, 0, 0);
+    issue(r1, 1, 1);
+    if constexpr (kDA == 3)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dma(2, i);
+    // the scale copy and the weights of unit 0 have landed (after them: the
+    // prologue's later loads); the barrier makes every wave's scales visible
+    if constexpr (kDA == 3) __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    tie(r0);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const half_t h = scale(j, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) fb[j][e] = decode_pair(r0, j, 0, e, h);
+    }
+    for (int u = 0; u < units; u += 3) {
+      unit(u, r0, r1, r2);
+      if (u + 1 < units) unit(u + 1, r1, r2, r0);
+      if (u + 2 < units) unit(u + 2, r2, r0, r1);
+    }
+    // Drain the copies and loads past the end before LDS is reused.
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    tie(r0);
+    tie(r1);
+    tie(r2);
+  };
+  if (m0 + kPBM <= M && n0 + cb * 64 + 64 <= N) main_loop(std::true_type{});
+  else main_loop(std::false_type{});
+  __syncthreads();
+
+  // The two K halves: waves p = 1 hand their sums to waves p = 0 through LDS
+  // (32 KB per wave, lane-contiguous 16-byte slots), which add them.
+  float4_t* red = reinterpret_cast<float4_t*>(lds);
+  if (p == 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[(cb * 32 + i * 4 + j) * 64 + lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (p == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] += red[(cb * 32 + i * 4 + j) * 64 + lane];
+  }
+  // Lane holds rows 4 q4 + r of column r16 of each 16 x 16 tile.  EPI: the
+  // gate / up pair (columns 2c, 2c + 1) sits in lanes r16, r16 ^ 1.
+  auto value = [&](int i, int j, int r) {
+    if constexpr (EPI) {
+      const float g = acc[i][j][r];
+      const float up = __shfl_xor(g, 1, 64);
+      return g / (1.0f + expf(-g)) * up;
+    } else {
+      return acc[i][j][r];
+    }
+  };
+  constexpr int kOutCols = EPI ? kPBN / 2 : kPBN;
+  constexpr int kOutEs = OD == LQ_F32 ? 4 : 2;
+  const int out_n = EPI ? N / 2 : N;
+  const int on0 = EPI ? n0 / 2 : n0;
+  // Whole tiles with 16-byte aligned output rows are staged in LDS row by row
+  // (the first kPBM x kOutCols x kOutEs bytes) and stored by all 8 waves in
+  // 16-byte pieces; other tiles store element by element.
+  const bool staged = m0 + kPBM <= M && on0 + kOutCols <= out_n &&
+                      (uint32_t(out_n) * kOutEs) % 16u == 0 &&
+                      (reinterpret_cast<uintptr_t>(O) & 15u) == 0;
+  if (staged) {
+    __syncthreads();   // every wave is done with the partial sums in LDS
+    if (p == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float v = value(i, j, r);
+            const int m = i * 16 + q4 * 4 + r;
+            const int n = cb * 64 + j * 16 + r16;
+            if (!EPI || (r16 & 1) == 0)
+              store_out<OD>(lds, size_t(m) * kOutCols + (EPI ? n / 2 : n), v, 0);
+          }
+    }
+    __syncthreads();
+    constexpr int kRowPieces = kOutCols * kOutEs / 16;
+    for (int idx = tid; idx < kPBM * kRowPieces; idx += 512) {
+      const int m = idx / kRowPieces, c = idx - m * kRowPieces;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + size_t(idx) * 16);
+      *reinterpret_cast<u32x4_t*>(static_cast<uint8_t*>(O) +
+                                  (size_t(m0 + m) * out_n + on0) * kOutEs + size_t(c) * 16) = v;
+    }
+    return;
+  }
+  if (p == 1) return;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + i * 16 + q4 * 4 + r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + cb * 64 + j * 16 + r16;
+        const float v = value(i, j, r);
+        if constexpr (EPI) {
+          if ((r16 & 1) == 0 && m < M && n < N) store_out<OD>(O, size_t(m) * (N / 2) + n / 2, v, 0);
+        } else {
+          if (m < M && n < N) store_out<OD>(O, size_t(m) * N + n, v, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Activation ring units for a tile whose scale rows take `sbytes` of LDS:
+// four (32 KB of scales) or three (64 KB); 0 = the scales do not fit.
+static int pair_slots(int64_t sbytes) {
+  return sbytes <= kPLds - 4 * 32768 ? 4 : sbytes <= kPLds - 3 * 32768 ? 3 : 0;
+}
+
+template <int SD, int OD, bool EPI>
+static int launch_gemm_pair(const void* X, const void* W, const void* S, void* O, int64_t M,
+                            int64_t N, int64_t K, int64_t G, hipStream_t st) {
+  int lg = 0;
+  while ((int64_t(1) << lg) < G) ++lg;
+  const int tiles_m = int((M + kPBM - 1) / kPBM);
+  const int tiles_n = int((N + kPBN - 1) / kPBN);
+  const int64_t es = SD == LQ_F32 ? 4 : 2;
+  const dim3 grid(unsigned(tiles_m * tiles_n)), block(512);
+  if (pair_slots(kPBN * (K / G) * es) == 4)
+    hipLaunchKernelGGL((gemm_w4p_kernel<SD, OD, EPI, 4>), grid, block, 0, st,
+                       static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
+                       int(N), int(K), int(K / G), lg, tiles_m, tiles_n);
+  else
+    hipLaunchKernelGGL((gemm_w4p_kernel<SD, OD, EPI, 3>), grid, block, 0, st,
+                       static_cast<const half_t*>(X), static_cast<const uint8_t*>(W), S, O, int(M),
+                       int(N), int(K), int(K / G), lg, tiles_m, tiles_n);
+  return check_launch();
+}
+
+// Whether the pair-split kernel takes this int4 / fp16-activation shape: its
+// layout limits (K % 128, power-of-two G >= 16, the tile's scale rows within
+// 64 KB of LDS, buffers below 4 GB) and enough 128 x 256 tiles to give every
+// CU one.
+static bool pair_applies(int64_t M, int64_t N, int64_t K, int64_t G, int sd) {
+  if (K % kPUnit != 0 || G < 16 || (G & (G - 1)) != 0 || K % G != 0) return false;
+  const int64_t es = sd == LQ_F32 ? 4 : 2;
+  if (pair_slots(kPBN * (K / G) * es) == 0) return false;
+  const int64_t lim = int64_t(1) << 32;
+  if (M * K * 2 >= lim || N * (K / 2) >= lim || (N + kPBN) * (K / G) * es >= lim) return false;
+  return ((M + kPBM - 1) / kPBM) * ((N + kPBN - 1) / kPBN) >= 256;
+}
+
 #ifndef LQ_GEMM_CFG
 #define LQ_GEMM_CFG 4, 2, 4, 4
 #endif
@@ -746,6 +1166,10 @@ template <int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, int64_t M,
                          int64_t N, int64_t K, int64_t G, hipStream_t st,
                          const FixedScratch* fixed = nullptr, int sd_rt = 0, int od_rt = 0) {
+  if constexpr (WBITS == 4 && XD == LQ_F16 && SD != kRT && OD != kRT) {
+    if (pair_applies(M, N, K, G, SD))
+      return launch_gemm_pair<SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+  }
   const int need = min_splits<WBITS, WBITS == 8 || XD == LQ_BF16>(K, G);
   if (need == 0) return LQ_ERR_SHAPE;
   // 256-row tiles only when they alone give every CU (256) a tile; below that

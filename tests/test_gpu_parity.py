@@ -185,9 +185,8 @@ def test_matvec_fp16_small(policy, wbits, M, N, K, G):
     (5, 250, 4096, 16), (16, 11008, 1024, 128), (12, 96, 2560, 512), (9, 13000, 1024, 64)])
 def test_matvec_lds_ring_shapes(wbits, M, N, K, G):
     """Decode sizes 2 <= M <= 16 with whole 512-byte row chunks (the LDS-ring
-    kernel): ragged N, odd chunk counts, post-scaled and pre-scaled groups."""
-    if wbits == 4 and G % 32:
-        pytest.skip("int4 groups hold whole 32-k lane spans")
+    kernel): ragged N, odd chunk counts, post-scaled and pre-scaled groups
+    (int4 G = 16 takes the LDS kernel instead)."""
     X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=7 * M + N + K)
     got = _matvec(wbits, X, W, S, N, K, G, "f16")
     _close(got, _oracle(wbits, X, W, S, G))
@@ -208,9 +207,7 @@ def test_matvec_many_rows_and_per_channel(wbits, M, N, K, G):
     At 16 < M <= 64 the int8 kernel sums whole-chunk groups (G % 256 == 0:
     768 = 3 chunks, per-channel) before scaling and scales other groups
     (384, 128, ...) every chunk; each workgroup starts at a different chunk,
-    so the group walks wrap."""
-    if wbits == 4 and G % 32:
-        pytest.skip("int4 groups hold whole 32-k lane spans")
+    so the group walks wrap.  int4 G = 16 takes the skinny kernel."""
     X, W, S = synth.matvec_case(wbits, M, N, K, G, 0.001, 0.01, seed=3 * M + N + K)
     got = _matvec(wbits, X, W, S, N, K, G, "f16")
     _close(got, _oracle(wbits, X, W, S, G))
@@ -474,6 +471,36 @@ def test_cfg5a_prefill_full():
     _close(got, _oracle(4, X, W, S, c["G"]))     # every output (BLAS on the host)
 
 
+# Prefill on the 128 x 256 pair-split kernel (int4 weights, fp16 activations,
+# at least 256 tiles, K % 128 == 0, power-of-two G >= 16): ragged tiles in
+# both dimensions, output rows that are not 16-byte multiples (element
+# stores), both LDS splits (scale rows within 32 KB: four activation units;
+# within 64 KB: three), odd unit counts, fp32 / bf16 scales and outputs, more
+# workgroups than CUs with a tile count that is not a multiple of 8.
+@pytest.mark.parametrize("M,N,K,G,sd,od", [
+    (2000, 4100, 1024, 64, "f16", "f16"),
+    (1100, 8192, 640, 32, "f32", "f32"),
+    (2048, 4096, 4096, 32, "bf16", "bf16"),
+    (1024, 8192, 2048, 16, "f16", "f16"),
+    (1030, 8200, 384, 128, "f16", "f32"),
+    (2560, 4352, 512, 128, "f16", "bf16"),
+])
+def test_prefill_pair_kernel(M, N, K, G, sd, od):
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, s_dtype=np.float32, seed=M + N + G)
+    if sd == "bf16":
+        S_used = ref.bf16_bits_to_f32(ref.f32_to_bf16_bits(S)).reshape(S.shape)
+        Sg = _up(S, "bf16")
+    else:
+        S_used = S.astype(NP_OF[sd]).astype(np.float32)
+        Sg = _up(S.astype(NP_OF[sd]))
+    Og = lq.empty((M, N), _dtype(od))
+    lq.dequant_matvec_int4[(N,), (128,)](_up(X), _up(W), Sg, Og, K, K // 2, K // G, G)
+    got = Og.numpy()
+    if od == "bf16":
+        got = ref.bf16_bits_to_f32(got).reshape(M, N)
+    _close(got, _oracle(4, X, W, S_used, G))
+
+
 def test_reference_fp32_matvec_api():
     """examples/38_quantized_matmul.py:312-321 flow: quantize_int4, then gpu_matvec_int4."""
     rng = np.random.default_rng(42)
@@ -549,6 +576,8 @@ def _silu_mul_oracle(X, Wg, Sg, Wu, Su, G):
     (64, 520, 768, 32, "f16"),
     (96, 600, 1024, 32, "f16"),     # prefill GEMM epilogue, k split
     (300, 1100, 512, 64, "f16"),    # prefill GEMM epilogue, ragged tiles
+    (2048, 2048, 1024, 64, "f16"),  # 128 x 256 pair-split kernel epilogue (staged stores)
+    (2000, 2050, 512, 32, "f16"),   # pair-split kernel, ragged tiles (element stores)
     (1100, 2048, 1024, 128, "f16"), # 256-row tiles
     (40, 300, 576, 32, "f16"),      # no fused kernel: staged fp32 matvec + pairwise epilogue
     (1, 700, 11008, 32, "f16"),     # row kernel at 6 segments with the epilogue
