@@ -95,8 +95,11 @@ int locomp_amd_get_policy(void);
  * device (all streams of the device if all_streams != 0), including buffers
  * superseded when a workspace grew; waits for the device to be idle first.
  * The next call that needs a workspace allocates it again.  A HIP graph
- * captured before the release that names one of them must not be replayed.
- * No counterpart in the reference (which allocates nothing across calls). */
+ * captured before the release that names one of them must not be replayed,
+ * and no other library call may run on that device concurrently with the
+ * release (a call on another host thread may already hold a workspace
+ * pointer that the release frees).  No counterpart in the reference (which
+ * allocates nothing across calls). */
 int locomp_amd_release_workspaces(void* stream, int all_streams);
 
 /* Dequantize int4 -> OUT [N, K].
@@ -150,13 +153,17 @@ int locomp_amd_dequant_matvec_int4(const void* X, const void* W,
 
 /* As locomp_amd_dequant_matvec_int4, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc).  No counterpart in the reference.  Same kernels and
- * results; the split-K prefill's fp32 partials (and the bf16 part rows of
- * fp32 activations at M <= 4) go to a fixed 32 MiB array in the library's
- * device memory (one per GPU, held until the process ends) instead of the
- * per-stream workspaces, and the call allocates nothing.  A
- * call whose split-K plan needs more (M x N x 4 bytes x splits: e.g. beyond
- * M = 512 at N = 4096) returns LQ_ERR_SCRATCH and launches nothing.  All calls
+ * forbid hipMalloc).  No counterpart in the reference.  Same kernels; the
+ * split-K prefill's fp32 partials (and the bf16 part rows of fp32 activations
+ * at M <= 4) go to a fixed 32 MiB array in the library's device memory (one
+ * per GPU, held until the process ends) instead of the per-stream workspaces,
+ * and the call allocates nothing.  Where the allocating entry would split K
+ * only for speed and the partials (M x N x 4 bytes x splits) exceed the
+ * array, this entry runs the unsplit GEMM instead (same results to the
+ * matmul tolerance, not bit for bit).  It returns LQ_ERR_SCRATCH, launching
+ * nothing, only when a split is required and does not fit: bf16 activations
+ * whose groups per split exceed what the GEMM stages (more than 64 scale
+ * groups in K, e.g. K = 8192 with G = 32 at M x N > 2 M outputs).  All calls
  * on one GPU share its array: calls that overlap in time on one GPU (several
  * streams or threads) race and must be serialised by the caller. */
 int locomp_amd_dequant_matvec_int4_noalloc(const void* X, const void* W,

@@ -679,47 +679,21 @@ __global__ __launch_bounds__(512, 1) void gemm_w4p_kernel(
       if constexpr (FULL) r.b[j] = bload_b64(wrsrc, bv0, kb + uint32_t(j * 16) * row_bytes);
       else r.b[j] = bload_b64(wrsrc, uint32_t(min(nb + 16 * j, N - 1)) * row_bytes + uint32_t(q4 * 8), kb);
     };
-    // Weights of unit u, then the activation copy of unit ud into its ring
-    // slot (units past the end re-read the last unit into slots no one reads
-    // again).
-    auto issue = [&](PSet& r, int u, int ud) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bload(r, u, j);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dma(ud, i);
-    };
-    // Per unit each wave issues 4 weight loads (during the first 32-k block)
-    // then 4 activation copies (during the second), and every wait below is
-    // exact under in-order completion:
-    //  * top of unit u: the copy of unit u has landed: after it come the
-    //    kDA - 1 later units' 8 loads (units 0 and 1 with kDA = 3: the 12 loads
-    //    of the prologue's tail);
-    //  * middle of unit u: the weights of unit u + 1 have landed: after them
-    //    come one copy (4) and unit u's weight loads (4) (at unit 0 this also
-    //    waits for a prologue copy).
-    // After the barrier every wave's copy of unit u is in LDS and no wave
-    // still reads unit u - 1, whose slot then takes unit u + kDA.  Unit u's
-    // first 32-k block is decoded (into fb) during unit u - 1.  The loads are
-    // spread over the MFMAs, one per row tile: issued all at once, the 8
-    // waves' 64 loads queue in the CU's memory pipeline and stall the waves'
-    // issue (in-kernel timestamps: a quarter of the loop).
     u32x4_t fb[4];
-    auto unit = [&](int u, PSet& cur, PSet& nxt, PSet& fut) {
-      if (kDA == 3 && u < 2) __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory");
-      else if constexpr (kDA == 3) __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory");
-      else __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      __syncthreads();
+    h8 fa[8];
+    u32x4_t fc[4];
+    // Block t = 0 of unit u (after the barrier that makes its copy visible):
+    // under row tile i, its t = 1 fragment, two pairs of the t = 1 weights of
+    // column tile i / 2, and (i < 4) one activation copy of unit u + kDA, whose
+    // slot (that of unit u - 1) no wave reads any more.
+    auto block0 = [&](int u, const PSet& cur) __attribute__((always_inline)) {
       const half_t* a = As[(u % SLOTS) * 2 + p];
-      h8 fa[8];
-      u32x4_t fc[4];
       half_t hs[4];
 #pragma unroll
       for (int i = 0; i < 8; ++i) fa[i] = read_a(a, i, 0);
 #pragma unroll
       for (int j = 0; j < 4; ++j) hs[j] = scale(j, u);
       __builtin_amdgcn_sched_barrier(0);
-      // block t = 0; under row tile i: its t = 1 fragment, two pairs of the
-      // t = 1 weights of column tile i / 2, and one load
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
 #pragma unroll
@@ -731,16 +705,18 @@ __global__ __launch_bounds__(512, 1) void gemm_w4p_kernel(
         fc[jj][e0] = decode_pair(cur, jj, 1, e0, hs[jj]);
         fc[jj][e0 + 1] = decode_pair(cur, jj, 1, e0 + 1, hs[jj]);
         interleave_mfma4<1, 2>();
-        if (i < 4) bload(fut, u + 2, i);
+        if (i < 4) dma(u + kDA, i);
         __builtin_amdgcn_sched_barrier(0);
       }
-      __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      tie(nxt);
+    };
+    // Block t = 1 of unit u: under row tile i, two pairs of unit u + 1's t = 0
+    // weights of column tile i / 2 and (i < 4) one weight load of unit u + 2
+    // into `fut` (unit u's set).
+    auto block1 = [&](int u, const PSet& nxt, PSet& fut) __attribute__((always_inline)) {
+      half_t hs[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) hs[j] = scale(j, u + 1 < units ? u + 1 : u);
       __builtin_amdgcn_sched_barrier(0);
-      // block t = 1; under row tile i: two pairs of unit u + 1's t = 0
-      // weights of column tile i / 2
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
 #pragma unroll
@@ -751,18 +727,77 @@ __global__ __launch_bounds__(512, 1) void gemm_w4p_kernel(
         fb[jj][e0] = decode_pair(nxt, jj, 0, e0, hs[jj]);
         fb[jj][e0 + 1] = decode_pair(nxt, jj, 0, e0 + 1, hs[jj]);
         interleave_mfma4<0, 2>();
-        if (i < 4) dma(u + kDA, i);
+        if (i < 4) bload(fut, u + 2, i);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    PSet r0, r1, r2;
-    issue(r0, 0, 0);
-    issue(r1, 1, 1);
-    if constexpr (kDA == 3)
+    // The two waves of a column block run half a unit apart, so that one of
+    // them is always in the pure-MFMA block t = 1 while the other reads its
+    // fragments and issues copies (started together after each barrier, both
+    // stall on the same LDS reads).  Waves p = 0 run barrier u, block 0 and
+    // block 1 of unit u; waves p = 1 run block 0 of unit u, barrier u + 1,
+    // block 1 of unit u (after barrier 0 at the start; the last unit has no
+    // barrier).  Both read unit u's fragments only after barrier u and are
+    // done with unit u - 1's before barrier u + 1.  Each wave counts its own
+    // loads, issued as B0 B1 D0 D1 [D2] (prologue), then D(u + kDA) B(u + 2)
+    // per unit (D: 4 copies, B: 4 weight loads); every wait is exact under
+    // in-order completion:
+    //  * before barrier u, the copy D(u) has landed.  p = 0 (after unit
+    //    u - 1): kDA = 3: 8 / 12 / 16 / 20 loads after it at u = 0 / 1 / 2 /
+    //    later; kDA = 2: 4 / 8 / 12.  p = 1 (after block 0 of unit u - 1,
+    //    before barrier u): kDA = 3: 8 (u = 0, 1), 12 (u = 2), 16; kDA = 2: 4
+    //    (u = 0, 1), 8;
+    //  * before block 1 of unit u, the weights B(u + 1): after them only the
+    //    copy D(u + kDA) (4).
+    auto top_wait = [&](int u) __attribute__((always_inline)) {
+      if (p == 0) {
+        if constexpr (kDA == 3) {
+          if (u == 0) __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+          else if (u == 1) __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory");
+          else if (u == 2) __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory");
+          else __asm__ volatile("s_waitcnt vmcnt(20)" ::: "memory");
+        } else {
+          if (u == 0) __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
+          else if (u == 1) __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+          else __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory");
+        }
+      } else {
+        if constexpr (kDA == 3) {
+          if (u <= 1) __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+          else if (u == 2) __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory");
+          else __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        } else {
+          if (u <= 1) __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
+          else __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        }
+      }
+    };
+    auto unit = [&](int u, PSet& cur, PSet& nxt) __attribute__((always_inline)) {
+      if (p == 0) {
+        top_wait(u);
+        __syncthreads();
+      }
+      block0(u, cur);
+      if (p == 1 && u + 1 < units) {
+        top_wait(u + 1);
+        __syncthreads();
+      }
+      __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      tie(nxt);
+      block1(u, nxt, cur);
+    };
+    PSet r0, r1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dma(2, i);
-    // the scale copy and the weights of unit 0 have landed (after them: the
-    // prologue's later loads); the barrier makes every wave's scales visible
+    for (int j = 0; j < 4; ++j) bload(r0, 0, j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bload(r1, 1, j);
+#pragma unroll
+    for (int d = 0; d < kDA; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dma(d, i);
+    // the scale copy and the weights of unit 0 have landed (after them: B1
+    // and the kDA prologue copies); the barrier makes every wave's scales
+    // visible
     if constexpr (kDA == 3) __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory");
     else __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory");
     tie(r0);
@@ -773,16 +808,18 @@ __global__ __launch_bounds__(512, 1) void gemm_w4p_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) fb[j][e] = decode_pair(r0, j, 0, e, h);
     }
-    for (int u = 0; u < units; u += 3) {
-      unit(u, r0, r1, r2);
-      if (u + 1 < units) unit(u + 1, r1, r2, r0);
-      if (u + 2 < units) unit(u + 2, r2, r0, r1);
+    if (p == 1) {   // barrier 0
+      top_wait(0);
+      __syncthreads();
+    }
+    for (int u = 0; u < units; u += 2) {
+      unit(u, r0, r1);
+      if (u + 1 < units) unit(u + 1, r1, r0);
     }
     // Drain the copies and loads past the end before LDS is reused.
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     tie(r0);
     tie(r1);
-    tie(r2);
   };
   if (m0 + kPBM <= M && n0 + cb * 64 + 64 <= N) main_loop(std::true_type{});
   else main_loop(std::false_type{});
@@ -1189,7 +1226,9 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
   if (big_tiles >= 128 && need <= 2 && (K / kBK) % 2 == 0 && K / kBK >= 8) {
     const int rc = launch_gemm_split<GemmDefault, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G, 2,
                                                                           st, fixed, sd_rt, od_rt);
-    if (rc != LQ_ERR_SHAPE || need > 1) return rc;
+    // no workspace, or the caller's fixed scratch too small (nothing was
+    // launched): the split is optional when need == 1, so go on unsplit
+    if ((rc != LQ_ERR_SHAPE && rc != LQ_ERR_SCRATCH) || need > 1) return rc;
   }
   const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
                         ((N + GemmSmall::BN - 1) / GemmSmall::BN);
@@ -1197,7 +1236,7 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
   if (splits > 1) {
     const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G,
                                                                         splits, st, fixed, sd_rt, od_rt);
-    if (rc != LQ_ERR_SHAPE || need > 1) return rc;
+    if ((rc != LQ_ERR_SHAPE && rc != LQ_ERR_SCRATCH) || need > 1) return rc;
   }
   return launch_gemm_cfg<GemmSmall, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G, 1, st, sd_rt,
                                                            od_rt);

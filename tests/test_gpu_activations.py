@@ -271,6 +271,41 @@ def test_fp32_split_is_exact_on_hard_values_m3():
         assert np.abs(got[m] - want).max() <= 2e-5 * np.abs(X[m].astype(np.float64)).sum()
 
 
+@pytest.mark.parametrize("M", [8, 64])
+def test_fp32_stacked_route_tiny_and_mixed_magnitudes(M):
+    """fp32 activations beyond four rows run as three bf16 part rows each
+    (x = hi + mid + lo) on the bf16 MFMA route, whose fp32 part-row products
+    are added as (P0 + P1) + P2.  Even rows hold activations of magnitude
+    ~1e-36, whose mid and lo parts lie below bf16's normal range (2^-126);
+    odd rows spread over 2^-30 .. 2^30 within the row.  Against the generic
+    fp32 kernel (one fp32 FMA chain per output) and a float64 oracle, each
+    output stays within 2e-5 of sum_k |x_k w_nk| of its row: a flushed mid
+    part would err by up to 2^-8 of the tiny rows' terms."""
+    rng = np.random.default_rng(40 + M)
+    N, K, G = 2048, 2048, 32
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    X[0::2] *= np.float32(1e-36)
+    X[1::2] *= np.exp2(rng.integers(-30, 30, (M // 2, K))).astype(np.float32)
+    W = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    S = rng.uniform(0.001, 0.01, (N, K // G)).astype(np.float32)
+    got = _run(4, X, W, S, N, K, G, "f32", "f32", "f32").astype(np.float64)
+    lq.set_policy(1)
+    try:
+        gen = _run(4, X, W, S, N, K, G, "f32", "f32", "f32").astype(np.float64)
+    finally:
+        lq.set_policy(0)
+    q = np.empty((N, K), np.float64)
+    q[:, 0::2] = (W & 15).astype(np.float64) - 8
+    q[:, 1::2] = (W >> 4).astype(np.float64) - 8
+    Wd = q * np.repeat(S.astype(np.float64), G, axis=1)
+    X64 = X.astype(np.float64)
+    want = X64 @ Wd.T
+    mag = np.abs(X64) @ np.abs(Wd).T
+    assert (np.abs(got - want) <= 2e-5 * mag).all(), np.max(np.abs(got - want) / mag)
+    assert (np.abs(got - gen) <= 2e-5 * mag).all(), np.max(np.abs(got - gen) / mag)
+    assert (np.abs(gen - want) <= 2e-5 * mag).all()
+
+
 def test_fp32_activations_in_graph_on_a_fresh_stream():
     """A capture on a stream with no workspace yet cannot allocate the part
     rows: the tile kernel then splits the activations itself (a new torch

@@ -72,13 +72,32 @@ def test_noalloc_fp32_activations_matches_allocating_entry():
         assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
 
 
-def test_noalloc_rejects_plans_beyond_the_scratch():
-    # 768 x 8192 takes 256-row tiles with k split in two: 768 * 8192 * 4 * 2 B
-    # = 48 MiB of partials, more than the fixed 32 MiB array
+def test_noalloc_runs_unsplit_when_the_optional_split_does_not_fit():
+    """512 x 14336 x 4096 int4 takes 256-row tiles with k split in two in the
+    allocating entry (58.7 MB of partials); the split is only for speed, so
+    with the fixed 32 MiB array the unsplit GEMM runs instead: different
+    summation order, the same results to the matmul tolerance.  A second,
+    smaller call follows."""
+    from oracle import quant_ref as ref
     lib = _lib.load()
-    M, N, K, G = 768, 8192, 4096, 128
+    for seed, (M, N, K, G) in enumerate(((512, 14336, 4096, 128), (512, 11008, 4096, 128))):
+        print(f"noalloc unsplit case M={M} N={N} K={K} G={G}", flush=True)
+        X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=20 + seed)
+        rc, got = _run(lib.locomp_amd_dequant_matvec_int4_noalloc, X, W, S, M, N, K, G)
+        assert rc == 0
+        np.testing.assert_allclose(got.astype(np.float32), ref.fast_numpy_matvec_int4(X, W, S, G),
+                                   rtol=1e-2, atol=1e-2)
+
+
+def test_noalloc_rejects_required_splits_beyond_the_scratch():
+    # bf16 activations post-scale their groups per split, which holds at most
+    # 64 groups: K = 8192 with G = 32 (256 groups) needs 4 splits, and
+    # 1024 x 4096 x 4 B x 4 = 64 MiB of partials exceed the fixed array
+    lib = _lib.load()
+    M, N, K, G = 1024, 4096, 8192, 32
     X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, seed=3)
-    rc, _ = _run(lib.locomp_amd_dequant_matvec_int4_noalloc, X, W, S, M, N, K, G)
+    Xb = (X.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)   # bf16 bits (truncated)
+    rc, _ = _run(lib.locomp_amd_dequant_matvec_int4_noalloc, Xb, W, S, M, N, K, G, _lib.BF16)
     assert rc == _lib.ERR_SCRATCH
-    rc, _ = _run(lib.locomp_amd_dequant_matvec_int4, X, W, S, M, N, K, G)
+    rc, _ = _run(lib.locomp_amd_dequant_matvec_int4, Xb, W, S, M, N, K, G, _lib.BF16)
     assert rc == 0
