@@ -148,71 +148,6 @@ class QuantCase:
             raise RuntimeError(f"launch failed: {rc}")
 
 
-class Stack:
-    """SmolLM2-135M-shaped decode linear stack: 30 layers x 7 int4 g32 GEMVs
-    (q, k, v, o, gate, up, down) at M = 1, random weights (BASELINE config 5b).
-    One step = all 210 GEMVs of one token, launched back to back (in a graph)."""
-
-    def __init__(self, seed=0, G=32, fused=False, silu=False, chain=False, f32=False):
-        """chain=True (with fused and silu) feeds every launch the previous
-        one's output, in the order examples/54_smollm2_inference.py:494-554
-        runs the linears: q|k|v -> o (on the q part, standing in for the
-        attention output) -> gate|up with SiLU * mul -> down -> the next
-        layer's q|k|v.  Attention, norms and residual adds are not on the
-        quantized path and are left out."""
-        self.chain = chain and fused and silu
-        # f32=True: fp32 activations and outputs (the reference's tensor dtype)
-        self.dt = 0 if f32 else 1
-        adt = np.float32 if f32 else np.float16
-        """fused=True concatenates the weights of linears that read the same
-        activation (q|k|v: N = 960, gate|up: N = 3072): 4 GEMVs per layer.
-        silu=True (with fused) runs gate|up as the fused SiLU * mul launch
-        (interleaved rows, 1536 outputs), which also covers the reference's
-        separate silu_mul_kernel (examples/54:113-120)."""
-        import torch
-        from locomp_amd import synth, _lib
-        self.lib = _lib.load()
-        rng = np.random.default_rng(seed)
-        self.layers = []
-        self.algo_bytes = 0
-        xs = {}
-        for K in (576, 1536):
-            xs[K] = _dev(synth.activations(rng, 1, K, dtype=adt))
-        self.xs = xs
-        shapes = synth.SMOLLM2_LAYER
-        if fused:
-            (nq, k0), (nk, _), (nv, _), o, (ng, _), (nu, _), down = shapes
-            shapes = [(nq + nk + nv, k0), o, (ng + nu, k0), down]
-        prev = self.xs[576]
-        for _ in range(synth.SMOLLM2_LAYERS):
-            for (N, K) in shapes:
-                W = synth.int4_weights(rng, N, K)
-                S = synth.scales(rng, N, K // G, 0.001, 0.01)
-                epi = silu and fused and N == 2 * 1536
-                O = torch.empty(N // 2 if epi else N, dtype=torch.float32 if f32 else torch.float16,
-                                device="cuda")
-                x = prev if self.chain else self.xs[K]
-                self.layers.append((N, K, G, _dev(W), _dev(S), O, epi, x))
-                self.algo_bytes += W.nbytes + S.nbytes + (K + (N // 2 if epi else N)) * (4 if f32 else 2)
-                prev = O     # (q|k|v: the o projection reads its first 576 = q)
-        self.R = 1
-        torch.cuda.synchronize()
-
-    def launch(self, i, stream):
-        vp = ctypes.c_void_p
-        for (N, K, G, W, S, O, epi, x) in self.layers:
-            if epi:
-                rc = self.lib.locomp_amd_dequant_matvec_int4_silu_mul(
-                    vp(x.data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
-                    K, K // 2, K // G, G, N // 2, 1, self.dt, 1, self.dt, stream)
-            else:
-                rc = self.lib.locomp_amd_dequant_matvec_int4(
-                    vp(x.data_ptr()), vp(W.data_ptr()), vp(S.data_ptr()), vp(O.data_ptr()),
-                    K, K // 2, K // G, G, N, 1, self.dt, 1, self.dt, stream)
-            if rc != 0:
-                raise RuntimeError(f"launch failed: {rc}")
-
-
 def time_graph(case, steps, warmup, trials=21, per_graph=None):
     """Median time of one launch, from `trials` replays of a graph of launches.
 
@@ -496,17 +431,22 @@ def main():
     if want("quantize"):
         run_case("quantize_int4_4096x4096_g32_from_f32", QuantCase(4096, 4096, 32), "hbm")
     if want("smollm2"):
+        # SmolLM2-135M-shaped decode step (locomp_amd.stack), every variant
+        # ending with the 49152 x 576 LM head; the chained ones run the
+        # reference's per-layer order with the RMSNorms and residual adds
+        from locomp_amd.stack import DecodeStack
         for fused, silu, chain, f32 in ((False, False, False, False), (True, False, False, False),
                                         (True, True, False, False), (True, True, True, False),
                                         (True, True, True, True)):
-            st = Stack(fused=fused, silu=silu, chain=chain, f32=f32)
+            st = DecodeStack(fused=fused, silu=silu, chain=chain, f32=f32)
             per, _ = time_graph(st, 4, 1)
             d = {"us_per_token": round(per * 1e6, 2), "GB_s": round(st.algo_bytes / per / 1e9, 1),
-                 "gemvs_per_token": len(st.layers), "algorithmic_bytes": st.algo_bytes,
-                 "us_per_gemv": round(per * 1e6 / len(st.layers), 3)}
-            name = "smollm2_135m_int4_g32_decode_stack" + ("_qkv_gateup_fused" if fused else "") + \
-                ("_silu_epilogue" if silu else "") + ("_chained" if chain else "") + \
-                ("_fp32_activations" if f32 else "")
+                 "gemvs_per_token": st.gemvs, "launches_per_token": len(st.links),
+                 "algorithmic_bytes": st.algo_bytes,
+                 "us_per_launch": round(per * 1e6 / len(st.links), 3)}
+            name = "smollm2_135m_int4_g32_decode_step" + ("_qkv_gateup_fused" if fused else "") + \
+                ("_silu_epilogue" if silu else "") + ("_chained_rmsnorm_residual" if chain else "") + \
+                "_lm_head" + ("_fp32_activations" if f32 else "")
             extra[name] = d
             log(name, d)
     if want("w8a16"):

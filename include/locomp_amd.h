@@ -256,6 +256,18 @@ int locomp_amd_quantize_int8(const void* W, void* Q, float* SCALES, int64_t N, i
  * ceiling the bandwidth-bound kernels above are compared against. */
 int locomp_amd_stream_read(const void* buf, int64_t bytes, void* sink, void* stream);
 
+/* Residual add + RMSNorm between the quantized linears of a decode step:
+ * for each of the M rows of K elements, H += R (when R is not null; H is
+ * updated in place), then Y = H * rsqrt(sum(H^2) / K + eps) * gamma.
+ * Replaces locomp_launch_rms_norm_kernel generated for
+ * examples/54_smollm2_inference.py:40-73 (args X, W, O, N, EPS_X1000 =
+ * eps * 1e6; grid (rows,), launched at :488-489) fused with
+ * locomp_launch_add_inplace_kernel (:164-167, the residual adds at :538 and
+ * :554).  H, R, gamma and Y share one dtype (LQ_F16 or LQ_F32); fp32
+ * arithmetic; Y may not alias H or R. */
+int locomp_amd_rms_norm(void* H, const void* R, const void* gamma, void* Y, int64_t M, int64_t K,
+                        float eps, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

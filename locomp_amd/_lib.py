@@ -50,6 +50,7 @@ SIGNATURES = {
     "locomp_amd_quantize_int4": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp],
     "locomp_amd_quantize_int8": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
     "locomp_amd_stream_read": [_vp, _i64, _vp, _vp],
+    "locomp_amd_rms_norm": [_vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _int, _vp],
 }
 
 _lib = None

@@ -37,6 +37,8 @@ int launch_split_f32_rows(const float*, void*, int64_t, int64_t, hipStream_t);
 int launch_rows_silu_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                        int64_t, int, int, int, hipStream_t);
 int launch_sum_part_rows(const float*, void*, int64_t, int64_t, int, hipStream_t);
+int launch_rms_norm(void*, const void*, const void*, void*, int64_t, int64_t, float, int,
+                    hipStream_t);
 int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
                     hipStream_t);
 int launch_silu_fast(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
@@ -404,6 +406,15 @@ int locomp_amd_quantize_int4(const void* W, void* PACKED, float* SCALES, int64_t
 int locomp_amd_quantize_int8(const void* W, void* Q, float* SCALES, int64_t N, int64_t K,
                              int64_t GROUP_SIZE, int in_dtype, void* stream) {
   return quantize_common(2, W, Q, SCALES, N, K, GROUP_SIZE, in_dtype, stream);
+}
+
+int locomp_amd_rms_norm(void* H, const void* R, const void* gamma, void* Y, int64_t M, int64_t K,
+                        float eps, int dtype, void* stream) {
+  if (dtype != LQ_F16 && dtype != LQ_F32) return LQ_ERR_DTYPE;
+  if (M < 0 || K < 0 || M > kMax32 || K > kMax32) return LQ_ERR_SHAPE;
+  if (M == 0 || K == 0) return LQ_OK;
+  if (!H || !gamma || !Y) return LQ_ERR_NULL;
+  return launch_rms_norm(H, R, gamma, Y, M, K, eps, dtype, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

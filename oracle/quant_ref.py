@@ -27,6 +27,11 @@ tests live in ``tests/test_oracle.py``):
   dot product, G=K -> per-channel).
 * ``quantize_*``: round trip dequant(quantize(w)) within s/2 per element and
   ties-to-even on constructed halfway inputs.
+* ``rms_norm_ref`` / ``residual_rms_norm_ref`` (the decode step around the
+  linears): closed form on constant rows (c w / sqrt(c^2 + eps)), a float64
+  scalar loop over the reference kernel's own loops, invariance of the
+  output under scaling the row when eps = 0, and the residual add as a
+  separate sum.
 """
 
 from __future__ import annotations
@@ -39,6 +44,7 @@ __all__ = [
     "numpy_matvec_int4", "numpy_matvec_int8",
     "fast_numpy_matvec_int4", "fast_numpy_matvec_int8",
     "quantize_int4", "quantize_int8", "quantize_int4_ref",
+    "rms_norm_ref", "residual_rms_norm_ref",
 ]
 
 
@@ -234,3 +240,30 @@ def quantize_int4_ref(w, group_size=32):
     q = np.clip(q, 0, 15).astype(np.uint8).reshape(N, K)
     packed = (q[:, 1::2] << 4) | q[:, 0::2]
     return packed.astype(np.uint8), scales.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# The decode step around the quantized linears (SmolLM2, examples/54).
+# ---------------------------------------------------------------------------
+
+def rms_norm_ref(x, w, eps=1e-5):
+    """Per row: out = x * rsqrt(sum(x^2) / N + eps) * w, in fp32
+    (examples/54_smollm2_inference.py:40-73: sum of squares at :49-51,
+    rsqrt(total / N + eps) at :65, val * rms * w at :73)."""
+    x = np.asarray(x, np.float32)
+    ss = np.sum(x * x, axis=-1, keepdims=True, dtype=np.float32)
+    rms = (np.float32(1.0) / np.sqrt(ss / np.float32(x.shape[-1]) + np.float32(eps))).astype(np.float32)
+    return (x * rms * np.asarray(w, np.float32)).astype(np.float32)
+
+
+def residual_rms_norm_ref(h, r, w, eps=1e-5, dtype=np.float32):
+    """The hidden-state update and norm between two linears of the decode
+    step: h += r (examples/54:164-167, the residual adds at :538 and :554)
+    stored in the activation dtype, then rms_norm_ref of the stored h.
+    Returns (new h, normed output), both in `dtype`."""
+    h32 = np.asarray(h, np.float32)
+    if r is not None:
+        h32 = h32 + np.asarray(r, np.float32)
+    h_new = h32.astype(dtype)
+    y = rms_norm_ref(h_new.astype(np.float32), np.asarray(w, dtype).astype(np.float32), eps)
+    return h_new, y.astype(dtype)

@@ -540,9 +540,11 @@ def test_all_q8_gives_zero(M, K):
 
 
 def test_smollm2_layer_shapes_int4_g32():
-    """One SmolLM2-135M layer's seven linears (int4 g32, M = 1) and the LM-head shape."""
+    """One SmolLM2-135M layer's seven linears (int4 g32, M = 1) and the LM head
+    over the tied embeddings (49152 x 576, examples/54_smollm2_inference.py:31,
+    573-574)."""
     from locomp_amd import synth as sy
-    for i, (N, K) in enumerate(sy.SMOLLM2_LAYER + [(4096, 576)]):
+    for i, (N, K) in enumerate(sy.SMOLLM2_LAYER + [(49152, 576)]):
         X, W, S = sy.matvec_case(4, 1, N, K, 32, 0.001, 0.01, seed=100 + i)
         got = _matvec(4, X, W, S, N, K, 32, "f16")
         _close(got, _oracle(4, X, W, S, 32))

@@ -226,3 +226,57 @@ def test_golden_fixtures():
                                    rtol=1e-5, atol=1e-6)
         np.testing.assert_allclose(ref.fast_numpy_matvec_int8(X, W8, S8, G), g[f"{tag}_y8"],
                                    rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- rms norm --
+
+def test_rms_norm_closed_form_constant_rows():
+    """A constant row c: rms = 1 / sqrt(c^2 + eps), out = c w / sqrt(c^2 + eps)."""
+    K, eps = 576, 1e-5
+    w = np.linspace(-2, 2, K).astype(np.float32)
+    for c in (0.0, 1.0, -3.5, 1e-3):
+        got = ref.rms_norm_ref(np.full((1, K), c, np.float32), w, eps)
+        want = c * w.astype(np.float64) / np.sqrt(c * c + eps)
+        np.testing.assert_allclose(got[0], want, rtol=1e-6, atol=1e-7)
+
+
+def test_rms_norm_matches_the_kernel_loops_in_float64():
+    """Scalar float64 restatement of examples/54:44-73: strided partial sums of
+    squares, total, rsqrt(total / N + eps), val * rms * w."""
+    rng = np.random.default_rng(11)
+    M, K, eps = 3, 200, 1e-5
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.standard_normal(K).astype(np.float32)
+    got = ref.rms_norm_ref(x, w, eps)
+    for m in range(M):
+        parts = [0.0] * 128
+        for tid in range(128):
+            for i in range(tid, K, 128):
+                parts[tid] += float(x[m, i]) ** 2
+        rms = 1.0 / np.sqrt(sum(parts) / K + eps)
+        want = [float(x[m, i]) * rms * float(w[i]) for i in range(K)]
+        np.testing.assert_allclose(got[m], want, rtol=2e-6, atol=1e-7)
+
+
+def test_rms_norm_scale_invariant_without_eps():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((2, 576)).astype(np.float32)
+    w = rng.standard_normal(576).astype(np.float32)
+    a = ref.rms_norm_ref(x, w, 0.0)
+    b = ref.rms_norm_ref(x * np.float32(64.0), w, 0.0)
+    np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)
+    # and a dropped square root or a missing mean would fail this
+    assert abs(float(np.sqrt(np.mean((a / w) ** 2))) - 1.0) < 1e-4
+
+
+def test_residual_rms_norm_adds_then_normalises():
+    rng = np.random.default_rng(13)
+    h = rng.standard_normal((1, 576)).astype(np.float16)
+    r = rng.standard_normal((1, 576)).astype(np.float16)
+    w = rng.standard_normal(576).astype(np.float16)
+    h_new, y = ref.residual_rms_norm_ref(h, r, w, 1e-5, np.float16)
+    assert np.array_equal(h_new, (h.astype(np.float32) + r.astype(np.float32)).astype(np.float16))
+    want = ref.rms_norm_ref(h_new.astype(np.float32), w.astype(np.float32), 1e-5).astype(np.float16)
+    assert np.array_equal(y, want)
+    h2, y2 = ref.residual_rms_norm_ref(h, None, w, 1e-5, np.float16)
+    assert np.array_equal(h2, h)
