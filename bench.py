@@ -206,8 +206,14 @@ class StreamCase:
             raise RuntimeError(f"stream_read failed: {rc}")
 
 
-def cpu_baseline(case, budget_s=20.0):
-    """Oracle (restated reference NumPy path) on the host, same inputs."""
+def cpu_baseline(case, budget_s=20.0, unit="GB/s"):
+    """Oracle (restated reference NumPy path) on the host, same inputs, timed
+    like the reference (examples/38_quantized_matmul.py:300-302, 323-340:
+    warm-ups, then the median of repeated calls): the dequant-matmul through
+    fast_numpy_matvec_int4 / int8 (:215-241), the dequantize through
+    dequant_int4_ref (examples/52_dequantize.py:129-143).  `unit` is the
+    metric of the GPU line it sits beside (GB/s of algorithmic bytes, or
+    TFLOP/s)."""
     from oracle import quant_ref as ref
     X, W, S = case.host
     try:
@@ -216,14 +222,26 @@ def cpu_baseline(case, budget_s=20.0):
     except Exception:
         blas_threads = int(os.environ.get("OPENBLAS_NUM_THREADS", os.environ.get("OMP_NUM_THREADS", "1")))
 
-    def run():
-        return ref.fast_numpy_matvec_int4(X[0].astype(np.float32), W, S.astype(np.float32), case.G)
+    if case.kind == "dequant":
+        what = "dequant_int4_ref (examples/52_dequantize.py:129-143)"
+
+        def run():
+            return ref.dequant_int4_ref(W, S, case.N, case.K, case.G).astype(np.float16)
+    else:
+        f = ref.fast_numpy_matvec_int4 if case.wbits == 4 else ref.fast_numpy_matvec_int8
+        what = (f"fast_numpy_matvec_int{case.wbits} (examples/38_quantized_matmul.py:"
+                f"{'215-232' if case.wbits == 4 else '235-241'})")
+        Xh = X.astype(np.float32)
+
+        def run():
+            return f(Xh if case.M > 1 else Xh[0], W, S.astype(np.float32), case.G)
 
     t0 = time.perf_counter()
     run()
     one = time.perf_counter() - t0
-    runs = int(max(3, min(15, budget_s / max(one, 1e-3) - 5)))
-    for _ in range(5):
+    warm = 5 if one < budget_s / 20 else 1
+    runs = int(max(3, min(15, budget_s / max(one, 1e-3) - warm)))
+    for _ in range(warm):
         run()
     ts = []
     for _ in range(runs):
@@ -231,15 +249,18 @@ def cpu_baseline(case, budget_s=20.0):
         run()
         ts.append(time.perf_counter() - t0)
     med = sorted(ts)[len(ts) // 2]
+    value = case.flops / med / 1e12 if unit == "TFLOP/s" else case.algo_bytes / med / 1e9
+    shape = (f"{case.N} x {case.K} g{case.G}" if case.kind == "dequant"
+             else f"M={case.M} x {case.K} x {case.N} g{case.G}")
+    threads = ("elementwise NumPy only, single-threaded" if case.kind == "dequant" else
+               f"elementwise NumPy is single-threaded, the BLAS product used {blas_threads} threads")
     return {
-        "value": round(case.algo_bytes / med / 1e9, 3), "unit": "GB/s",
-        "cores": int(blas_threads),
+        "value": round(value, 4), "unit": unit,
+        "cores": 1 if case.kind == "dequant" else int(blas_threads),
         "kind": "port",
-        "sample": (f"oracle fast_numpy_matvec_int4 (examples/38_quantized_matmul.py:215-232) on the "
-                   f"full M=1 x 4096 x 11008 g128 inputs, median of {runs} runs after 5 warm-ups, "
-                   f"{med * 1e3:.1f} ms/call; elementwise NumPy is single-threaded, the BLAS "
-                   f"product used {blas_threads} threads; host os.cpu_count()={os.cpu_count()}, "
-                   f"affinity={len(os.sched_getaffinity(0))}"),
+        "sample": (f"oracle {what} on the full {shape} inputs, median of {runs} runs after "
+                   f"{warm} warm-up(s), {med * 1e3:.1f} ms/call; {threads}; host "
+                   f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"),
     }
 
 
@@ -350,7 +371,7 @@ def main():
     def want(name):
         return only is None or name in only
 
-    def run_case(name, case, bound):
+    def run_case(name, case, bound, cpu=False):
         per, info = time_graph(case, max(20, case.R), 5)
         d = {"us_per_launch": round(per * 1e6, 3), "GB_s": round(case.algo_bytes / per / 1e9, 1),
              "replicas": case.R, **info}
@@ -360,6 +381,9 @@ def main():
             d["frac_hbm"] = round(case.algo_bytes / per / 1e9 / HBM_PEAK_GBS, 4)
         else:
             d["frac_mfma_f16"] = round(case.flops / per / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+        if cpu and not args.no_cpu:
+            # the reference's NumPy path beside this line, same inputs
+            d["cpu_baseline"] = cpu_baseline(case, 8.0, "GB/s" if bound == "hbm" else "TFLOP/s")
         extra[name] = d
         log(name, d)
 
@@ -367,7 +391,7 @@ def main():
         c = synth.CFG5A
         run_case("gemm_prefill_w4a16_2048x4096x4096_g128",
                  Case("matvec", 4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
-                      min_bytes=0, max_replicas=4), "mfma")
+                      min_bytes=0, max_replicas=4), "mfma", cpu=True)
     if want("gemm_prefill_w8"):
         c = synth.CFG5A
         run_case("gemm_prefill_w8a16_2048x4096x4096_g128",
@@ -427,7 +451,7 @@ def main():
     if want("dequant"):
         c = synth.CFG2
         run_case("dequant_int4_4096x4096_g32_f16",
-                 Case("dequant", 4, 0, c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm")
+                 Case("dequant", 4, 0, c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm", cpu=True)
     if want("quantize"):
         run_case("quantize_int4_4096x4096_g32_from_f32", QuantCase(4096, 4096, 32), "hbm")
     if want("smollm2"):
@@ -452,7 +476,7 @@ def main():
     if want("w8a16"):
         c = synth.CFG4
         run_case("w8a16_M64_14336x4096",
-                 Case("matvec", 8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm")
+                 Case("matvec", 8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"]), "hbm", cpu=True)
 
     cpu = None if args.no_cpu else cpu_baseline(head)
     traffic = None
