@@ -21,8 +21,8 @@
  *     grow-only workspaces per (device, stream): on the first prefill that
  *     splits K, on the first SiLU * mul call without a fused kernel, and on
  *     the first fp32-activation call (its bf16 part rows: 24 K bytes at
- *     M <= 4; at M > 4 3 M K x 2 bytes plus the parts' fp32 products,
- *     3 M N x 4 bytes, each at most 256 MB, larger M in row blocks); they
+ *     M <= 4; at M > 4 2 M K x 2 bytes plus the parts' fp32 products,
+ *     2 M N x 4 bytes, each at most 256 MB, larger M in row blocks); they
  *     are held until the process ends or locomp_amd_release_workspaces.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
  *     is asynchronous: the caller synchronises.
@@ -129,14 +129,17 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * Activations may be fp16, bf16 or fp32 (the reference's dtype): fp16 and
  * bf16 run on fp16 / bf16 matrix cores at every M (the row kernel at
  * M <= 2 with G % 32: bf16 dot products); fp32 at M <= 4 runs on bf16
- * matrix cores as three exact bf16 parts (split once per call into a
- * workspace, or inside the kernel on a capturing stream that has none yet
- * and on small matrices), except M = 1 with K <= 4096 where the segment
- * kernel does not apply (K < 2048 or G % 128 != 0), which takes fp32 FMAs
- * on the row kernel;
- * fp32 at M > 4 is split the same way into 3 M bf16 rows that take the bf16
- * route (3 M <= 16: the decode kernel; else the MFMA GEMM, G % 32 == 0)
- * with fp32 products, whose three part rows are then added; other fp32
+ * matrix cores: at M = 1 on the segment kernel (K >= 2048, G % 128 == 0) as
+ * two round-to-nearest bf16 parts (|x - hi - lo| <= 2^-16 |x|), at
+ * 2 <= M <= 4 (and M = 1 where the segment kernel does not apply) as three
+ * exact bf16 parts (split once per call into a workspace, or inside the
+ * kernel on a capturing stream that has none yet and on small matrices),
+ * except M = 1 with K <= 4096 where the segment kernel does not apply
+ * (K < 2048 or G % 128 != 0), which takes fp32 FMAs on the row kernel;
+ * fp32 at M > 4 is split into two round-to-nearest parts, 2 M bf16 rows
+ * that take the bf16 route (2 M <= 16: the decode kernel; else the MFMA
+ * GEMM, G % 32 == 0) with fp32 products, whose two part rows are then added
+ * (error at most 2^-16 sum_k |x_k w_nk| beyond fp32 summation); other fp32
  * shapes, and a capture on a stream without those workspaces, take a
  * generic kernel.  The fast kernels need X and W 16-byte aligned and the
  * scales 4-byte aligned (otherwise a generic kernel runs).

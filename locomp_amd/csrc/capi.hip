@@ -78,35 +78,37 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
                            int64_t G, int64_t N, int64_t M, int xd, int sd, int od, hipStream_t st,
                            const FixedScratch* fixed = nullptr);
 
-// fp32 activations at M > 4: each row split exactly into three bf16 parts
-// (hi + mid + lo, as the M <= 4 kernels do), stacked as 3 M bf16 rows in the
-// stream's workspace slot 2, run through the bf16 route with fp32 output
-// (slot 3), and the three part rows' products added in order.  Each part
-// times an integer weight is exact in fp32, so the result is an fp32 dot
-// product in a different summation order.  Taken only where the bf16 route
-// is a fast one (3 M <= 16: the tile kernel; else the MFMA GEMM, G % 32),
+// fp32 activations at M > 4: each row split into two bf16 parts with round
+// to nearest (hi = RN(x), lo = RN(x - hi): |x - hi - lo| <= 2^-16 |x|),
+// stacked as 2 M bf16 rows in the stream's workspace slot 2, run through the
+// bf16 route with fp32 output (slot 3), and the two part rows' products
+// added.  Each part times an integer weight is exact in fp32, so the result
+// differs from an fp32 dot product by at most 2^-16 sum_k |x_k w_nk| beyond
+// the summation order: no more than fp32 accumulation's own worst case
+// (K 2^-24 sum_k |x_k w_nk|) for K >= 256.  Taken only where the bf16 route
+// is a fast one (2 M <= 16: the tile kernel; else the MFMA GEMM, G % 32),
 // in row blocks whose buffers fit the workspace cap; LQ_ERR_SHAPE (the
 // caller falls back) when it does not apply or a workspace is missing (a
 // capture on a stream that has none yet).
 template <int WBITS>
 static int matmul_f32_stacked(const void* X, const void* W, const void* S, void* O, int64_t K,
                               int64_t G, int64_t N, int64_t M, int sd, int od, hipStream_t st) {
-  if (3 * M > 16 && (G % 32 != 0 || K % 64 != 0)) return LQ_ERR_SHAPE;
+  if (2 * M > 16 && (G % 32 != 0 || K % 64 != 0)) return LQ_ERR_SHAPE;
   // below ~2^24 multiply-adds its three launches cost more than the generic
-  // kernel (16 x 576 x 576: 20 us against 11)
+  // kernel (16 x 576 x 576 with three parts: 20 us against 11)
   if (M * N * K < (int64_t(1) << 24)) return LQ_ERR_SHAPE;
   constexpr int64_t kCap = int64_t(256) << 20;          // bytes per workspace slot
-  const int64_t rows = std::max<int64_t>(1, std::min(kCap / (3 * K * 2), kCap / (3 * N * 4)));
+  const int64_t rows = std::max<int64_t>(1, std::min(kCap / (2 * K * 2), kCap / (2 * N * 4)));
   const int64_t mb = std::min(M, rows);
-  void* parts = stream_workspace(2, size_t(3 * mb * K * 2), st);
-  void* prod = stream_workspace(3, size_t(3 * mb * N * 4), st);
+  void* parts = stream_workspace(2, size_t(2 * mb * K * 2), st);
+  void* prod = stream_workspace(3, size_t(2 * mb * N * 4), st);
   if (parts == nullptr || prod == nullptr) return LQ_ERR_SHAPE;
   const size_t osz = od == LQ_F32 ? 4 : 2;
   for (int64_t m0 = 0; m0 < M; m0 += mb) {
     const int64_t m = std::min(mb, M - m0);
     int rc = launch_split_f32_rows(static_cast<const float*>(X) + m0 * K, parts, m, K, st);
     if (rc != LQ_OK) return rc;
-    rc = matmul_dispatch<WBITS>(parts, W, S, prod, K, G, N, 3 * m, LQ_BF16, sd, LQ_F32, st);
+    rc = matmul_dispatch<WBITS>(parts, W, S, prod, K, G, N, 2 * m, LQ_BF16, sd, LQ_F32, st);
     if (rc != LQ_OK) return rc;
     rc = launch_sum_part_rows(static_cast<const float*>(prod),
                               static_cast<uint8_t*>(O) + size_t(m0 * N) * osz, m, N, od, st);
@@ -140,7 +142,7 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
     if (rc != LQ_ERR_SHAPE) return rc;
   }
   if (fast_common && xd == LQ_F32 && M > 4 && fixed == nullptr) {
-    // fp32 beyond the decode kernels' 4 rows: exact bf16 parts on the bf16 route
+    // fp32 beyond the decode kernels' 4 rows: two bf16 parts on the bf16 route
     const int rc = matmul_f32_stacked<WBITS>(X, W, S, O, K, G, N, M, sd, od, st);
     if (rc != LQ_ERR_SHAPE) return rc;
   }

@@ -23,15 +23,16 @@ constexpr int kSegOob = 0x40000000;
 
 // XD: activation dtype.  bf16 / fp32 activations run bf16 MFMAs on weights
 // decoded to bf16 128 + q (0x4300 | q, 7 VALU ops per dword); fp32 ones as
-// three exact bf16 parts (hi + mid + lo) whose MFMAs chain into the same
-// accumulator.  SD / OD = kRT take the dtypes from sd_rt / od_rt.
+// two bf16 parts (hi = RN(x), lo = RN(x - hi), |x - hi - lo| <= 2^-16 |x|)
+// whose MFMAs chain into the same accumulator.  SD / OD = kRT take the
+// dtypes from sd_rt / od_rt.
 template <int M_, int NSEG, int RW, int SD, int OD, bool PART, int XD = LQ_F16>
 __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
     const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
     int od_rt = 0) {
   constexpr bool kH = XD == LQ_F16;
-  constexpr int NP = XD == LQ_F32 ? 3 : 1;     // bf16 parts per activation
+  constexpr int NP = XD == LQ_F32 ? 2 : 1;     // bf16 parts per activation
   constexpr int kXB = XD == LQ_F32 ? 4 : 2;    // activation element bytes
   // load the output pointer now (else its kernel-argument load sits between
   // the final reduction and the store)
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(256, 2) void gemv_seg_kernel(
 #pragma unroll
           for (int p = 0; p < NP; ++p)
             xs_l[((m * NSEG + c) * NP + p) * 256 + t] =
-                __builtin_bit_cast(u32x4_t, TileMfma<4, LQ_F32>::prep_x(x8, p));
+                __builtin_bit_cast(u32x4_t, TileMfma<4, LQ_F32>::prep_x2(x8, p));
         }
       }
   }

@@ -159,6 +159,18 @@ template <> struct TileMfma<4, LQ_F32> : TileMfma<4, LQ_BF16> {
     v.w = __builtin_amdgcn_perm(b[7], b[3], 0x07060302u);
     return __builtin_bit_cast(bf8_t, v);
   }
+  // the same for part `part` of the two-way round-to-nearest split
+  __device__ static op_t prep_x2(const x_t& x, int part) {
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = f32_rn2_part_bits(x[i], part);
+    u32x4_t v;
+    v.x = __builtin_amdgcn_perm(b[4], b[0], 0x07060302u);
+    v.y = __builtin_amdgcn_perm(b[5], b[1], 0x07060302u);
+    v.z = __builtin_amdgcn_perm(b[6], b[2], 0x07060302u);
+    v.w = __builtin_amdgcn_perm(b[7], b[3], 0x07060302u);
+    return __builtin_bit_cast(bf8_t, v);
+  }
 };
 template <> struct TileMfma<8, LQ_F32> : TileMfma<8, LQ_BF16> {
   typedef u32x4_t x_t;

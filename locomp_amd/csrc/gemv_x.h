@@ -8,11 +8,13 @@ namespace lq {
 
 void* stream_workspace(int slot, size_t bytes, hipStream_t st);
 
-// fp32 activations X [M, K] -> their exact three-way bf16 split, P bf16 with
-// row m + pstride * part = part `part` of row m (pstride 4 for the tile
-// kernel's 12 part rows at M <= 4: rows of m >= M are not written and not
-// read; pstride M for the stacked [3 M, K] layout).  Thread i takes 8
-// consecutive k of one row.
+// fp32 activations X [M, K] -> their bf16 parts, P bf16 with row m + pstride
+// * part = part `part` of row m: NPARTS = 3, the exact three-way split (the
+// tile kernel's 12 part rows at M <= 4, pstride 4: rows of m >= M are not
+// written and not read); NPARTS = 2, the round-to-nearest two-way split (the
+// stacked [2 M, K] layout, pstride M).  Thread i takes 8 consecutive k of one
+// row.
+template <int NPARTS>
 static __global__ __launch_bounds__(256) void split_f32_parts_kernel(const float* __restrict__ X,
                                                              uint16_t* __restrict__ P, int M,
                                                              int K, int pstride) {
@@ -24,24 +26,25 @@ static __global__ __launch_bounds__(256) void split_f32_parts_kernel(const float
   const u32x4_t b = *reinterpret_cast<const u32x4_t*>(X + size_t(m) * K + k + 4);
   const uint32_t x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-  for (int p = 0; p < 3; ++p) {
+  for (int p = 0; p < NPARTS; ++p) {
     uint32_t h[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = f32_part_bits(x[e], p) >> 16;
+    for (int e = 0; e < 8; ++e)
+      h[e] = (NPARTS == 3 ? f32_part_bits(x[e], p) : f32_rn2_part_bits(x[e], p)) >> 16;
     const u32x4_t v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
                        h[6] | (h[7] << 16)};
     *reinterpret_cast<u32x4_t*>(P + (size_t(m) + size_t(pstride) * p) * K + k) = v;
   }
 }
 
-// O [M, N] = P[0] + P[1] + P[2] (the three part rows' fp32 products, [3, M, N],
-// added in that order), stored as od.
+// O [M, N] = P[0] + P[1] (the two part rows' fp32 products, [2, M, N], added in
+// that order), stored as od.
 static __global__ __launch_bounds__(256) void sum_part_rows_kernel(const float* __restrict__ P,
                                                            void* __restrict__ O, int64_t MN,
                                                            int od) {
   const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (e >= MN) return;
-  store_out<kRT>(O, size_t(e), (P[e] + P[MN + e]) + P[2 * MN + e], od);
+  store_out<kRT>(O, size_t(e), P[e] + P[MN + e], od);
 }
 
 template <int WBITS, int XD, int NSC>
@@ -235,7 +238,7 @@ int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_
   }
   if (parts) {
     const int threads = int(M * (K / 8));
-    hipLaunchKernelGGL(split_f32_parts_kernel, dim3((threads + 255) / 256), dim3(256), 0, st,
+    hipLaunchKernelGGL(split_f32_parts_kernel<3>, dim3((threads + 255) / 256), dim3(256), 0, st,
                        static_cast<const float*>(X), static_cast<uint16_t*>(parts), int(M), int(K), 4);
     X = parts;
     LQ_NSC(kXPre)

@@ -204,6 +204,18 @@ __device__ __forceinline__ uint32_t f32_part_bits(uint32_t x, int part) {
   return part == 0 ? hi : part == 1 ? mid : __float_as_uint(r2);
 }
 
+// Part `part` (0 hi, 1 lo) of the two-way bf16 split of fp32 x with round to
+// nearest even: hi = RN(x), lo = RN(x - hi) (x - hi is exact in fp32), as the
+// bf16 bit pattern in the high half of the returned dword.  |x - hi - lo| <=
+// 2^-16 |x|; at |x| >= 2^127 hi is truncated instead (RN could round to inf).
+__device__ __forceinline__ uint32_t f32_rn2_part_bits(uint32_t x, int part) {
+  const uint32_t rn = (x + 0x7FFFu + ((x >> 16) & 1u)) & 0xFFFF0000u;
+  const uint32_t hi = (x & 0x7F000000u) == 0x7F000000u ? x & 0xFFFF0000u : rn;
+  if (part == 0) return hi;
+  const uint32_t r = __float_as_uint(__uint_as_float(x) - __uint_as_float(hi));
+  return (r + 0x7FFFu + ((r >> 16) & 1u)) & 0xFFFF0000u;
+}
+
 constexpr float kInt4Bias = 1032.0f;
 constexpr float kInt8Bias = 1152.0f;
 
