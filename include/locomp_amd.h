@@ -21,8 +21,9 @@
  *     grow-only workspaces per (device, stream): on the first prefill that
  *     splits K, on the first SiLU * mul call without a fused kernel, and on
  *     the first fp32-activation call (its bf16 part rows: 24 K bytes at
- *     M <= 4; at M > 4 2 M K x 2 bytes plus the parts' fp32 products,
- *     2 M N x 4 bytes, each at most 256 MB, larger M in row blocks); they
+ *     M <= 4; at M > 4 2 M K x 2 bytes, plus the parts' fp32 products,
+ *     2 M N x 4 bytes, where 2 M <= 64; each at most 256 MB, larger M in
+ *     row blocks); they
  *     are held until the process ends or locomp_amd_release_workspaces.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
  *     is asynchronous: the caller synchronises.
@@ -137,8 +138,9 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * except M = 1 with K <= 4096 where the segment kernel does not apply
  * (K < 2048 or G % 128 != 0), which takes fp32 FMAs on the row kernel;
  * fp32 at M > 4 is split into two round-to-nearest parts, 2 M bf16 rows
- * that take the bf16 route (2 M <= 16: the decode kernel; else the MFMA
- * GEMM, G % 32 == 0) with fp32 products, whose two part rows are then added
+ * (row 2i + p = part p of row i) that take the bf16 route: 2 M <= 64 the
+ * decode kernels with fp32 products, whose two part rows a second launch
+ * adds; else the MFMA GEMM (G % 32 == 0), which adds them in its epilogue
  * (error at most 2^-16 sum_k |x_k w_nk| beyond fp32 summation); other fp32
  * shapes, and a capture on a stream without those workspaces, take a
  * generic kernel.  The fast kernels need X and W 16-byte aligned and the

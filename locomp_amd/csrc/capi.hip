@@ -18,6 +18,9 @@ template <int WBITS>
 int launch_gemm_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
                   int, int, int, hipStream_t, const FixedScratch*);
 template <int WBITS>
+int launch_gemm_f32_parts(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                          int64_t, int, int, hipStream_t);
+template <int WBITS>
 int launch_skinny_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                     int64_t, int, int, int, hipStream_t, const FixedScratch*);
 template <int WBITS>
@@ -80,9 +83,10 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
 
 // fp32 activations at M > 4: each row split into two bf16 parts with round
 // to nearest (hi = RN(x), lo = RN(x - hi): |x - hi - lo| <= 2^-16 |x|),
-// stacked as 2 M bf16 rows in the stream's workspace slot 2, run through the
-// bf16 route with fp32 output (slot 3), and the two part rows' products
-// added.  Each part times an integer weight is exact in fp32, so the result
+// as 2 M bf16 rows in the stream's workspace slot 2 (row 2i + p = part p of
+// row i) and run through the bf16 route: the MFMA GEMM adds the two part
+// rows' products in its epilogue (2 M > 64); the decode kernels write them
+// as fp32 (slot 3) and a second launch adds them.  Each part times an integer weight is exact in fp32, so the result
 // differs from an fp32 dot product by at most 2^-16 sum_k |x_k w_nk| beyond
 // the summation order: no more than fp32 accumulation's own worst case
 // (K 2^-24 sum_k |x_k w_nk|) for K >= 256.  Taken only where the bf16 route
@@ -101,17 +105,29 @@ static int matmul_f32_stacked(const void* X, const void* W, const void* S, void*
   const int64_t rows = std::max<int64_t>(1, std::min(kCap / (2 * K * 2), kCap / (2 * N * 4)));
   const int64_t mb = std::min(M, rows);
   void* parts = stream_workspace(2, size_t(2 * mb * K * 2), st);
-  void* prod = stream_workspace(3, size_t(2 * mb * N * 4), st);
-  if (parts == nullptr || prod == nullptr) return LQ_ERR_SHAPE;
+  if (parts == nullptr) return LQ_ERR_SHAPE;
   const size_t osz = od == LQ_F32 ? 4 : 2;
   for (int64_t m0 = 0; m0 < M; m0 += mb) {
     const int64_t m = std::min(mb, M - m0);
+    uint8_t* out = static_cast<uint8_t*>(O) + size_t(m0 * N) * osz;
     int rc = launch_split_f32_rows(static_cast<const float*>(X) + m0 * K, parts, m, K, st);
     if (rc != LQ_OK) return rc;
+    if (2 * m > 64) {
+      // the bf16 GEMM adds each row's two part products in its epilogue
+      rc = launch_gemm_f32_parts<WBITS>(parts, W, S, out, 2 * m, N, K, G, sd, od, st);
+      if (rc != LQ_ERR_SHAPE) {
+        if (rc != LQ_OK) return rc;
+        continue;
+      }
+    }
+    // decode-sized blocks (and a GEMM without its split workspace): the
+    // bf16 route into fp32 products, then the pair sum
+    // (without it the caller's fallback rewrites every row)
+    void* prod = stream_workspace(3, size_t(2 * mb * N * 4), st);
+    if (prod == nullptr) return LQ_ERR_SHAPE;
     rc = matmul_dispatch<WBITS>(parts, W, S, prod, K, G, N, 2 * m, LQ_BF16, sd, LQ_F32, st);
     if (rc != LQ_OK) return rc;
-    rc = launch_sum_part_rows(static_cast<const float*>(prod),
-                              static_cast<uint8_t*>(O) + size_t(m0 * N) * osz, m, N, od, st);
+    rc = launch_sum_part_rows(static_cast<const float*>(prod), out, m, N, od, st);
     if (rc != LQ_OK) return rc;
   }
   return LQ_OK;

@@ -124,7 +124,10 @@ __device__ __forceinline__ void xcd_tile(int b, int tiles_m, int tiles_n, int a_
 // O [M, N / 2] (columns n and n + 1 sit in lanes r16 and r16 ^ 1).
 // XD: activation dtype, fp16 (fp16 MFMA) or bf16 (bf16 MFMA; B holds the
 // exact integers q - 8 / q as bf16 and the scales are applied in fp32, like
-// int8).  SD / OD = kRT take the scale / output dtype from sd_rt / od_rt.
+// int8).  XD = LQ_F32: bf16 part rows of fp32 activations, the two parts of
+// row i at rows 2i and 2i + 1 (M counts part rows); the epilogue adds each
+// pair (rows 4 q + r and 4 q + r + 1 sit in one lane) and stores O [M / 2, N].
+// SD / OD = kRT take the scale / output dtype from sd_rt / od_rt.
 template <class C, int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
@@ -132,7 +135,9 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     int kspan, int sd_rt = 0, int od_rt = 0) {
   constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN;
   static_assert(BM % (8 * C::kWaves) == 0, "A DMA: whole 1 KB instructions per wave");
-  constexpr bool kBf = XD == LQ_BF16;
+  constexpr bool kParts = XD == LQ_F32;
+  constexpr bool kBf = XD == LQ_BF16 || kParts;
+  static_assert(!(kParts && EPI), "part rows take the plain epilogue");
   typedef typename Elem<SD == kRT ? LQ_F32 : SD>::T stype;
   __shared__ __attribute__((aligned(16))) half_t As[kAStages][BM * kBK];
   __shared__ __attribute__((aligned(16))) half_t Bs[kBStages][BN * kBK];
@@ -162,7 +167,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
   // slice blockIdx.y of O
   const int kbeg = blockIdx.y * kspan;
   kspan = min(kspan, K - kbeg);                // the last split may be shorter
-  const size_t obase = size_t(blockIdx.y) * M * N;
+  const size_t obase = size_t(blockIdx.y) * (kParts ? M / 2 : M) * N;
   const int wrow0 = wm * TM * 16;              // first tile row this wave multiplies
 
   // A DMA: wave w copies rows [w * kDmaRows, (w + 1) * kDmaRows) of the tile
@@ -486,6 +491,11 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
           const float up = __shfl_xor(g, 1, 64);
           if ((r16 & 1) == 0 && m < M && n < N)
             store_out<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up, od_rt);
+        } else if constexpr (kParts) {
+          // hi part + lo part (M even: row m + 1 < M with m)
+          if ((r & 1) == 0 && m < M && n < N)
+            store_out<OD>(O, obase + size_t(m >> 1) * N + n, acc[i][j][r] + acc[i][j][r + 1],
+                          od_rt);
         } else {
           if (m < M && n < N) store_out<OD>(O, obase + size_t(m) * N + n, acc[i][j][r], od_rt);
         }
@@ -1176,7 +1186,8 @@ template <class C, int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 static int launch_gemm_split(const void* X, const void* W, const void* S, void* O, int64_t M,
                              int64_t N, int64_t K, int64_t G, int splits, hipStream_t st,
                              const FixedScratch* fixed, int sd_rt = 0, int od_rt = 0) {
-  const size_t mn = size_t(M) * size_t(N);
+  // (part rows: the reduction sees the summed rows)
+  const size_t mn = size_t(XD == LQ_F32 ? M / 2 : M) * size_t(N);
   const size_t ws_bytes = mn * sizeof(float) * size_t(splits);
   void* ws;
   if (fixed != nullptr) {   // caller-provided scratch: never allocate
@@ -1207,7 +1218,7 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
     if (pair_applies(M, N, K, G, SD))
       return launch_gemm_pair<SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
   }
-  const int need = min_splits<WBITS, WBITS == 8 || XD == LQ_BF16>(K, G);
+  const int need = min_splits<WBITS, WBITS == 8 || XD != LQ_F16>(K, G);
   if (need == 0) return LQ_ERR_SHAPE;
   // 256-row tiles only when they alone give every CU (256) a tile; below that
   // (M <= 1024 at N = 4096) 128 x 128 tiles finish sooner, split over k when
@@ -1232,7 +1243,7 @@ static int launch_gemm_t(const void* X, const void* W, const void* S, void* O, i
   }
   const int64_t tiles = ((M + GemmSmall::BM - 1) / GemmSmall::BM) *
                         ((N + GemmSmall::BN - 1) / GemmSmall::BN);
-  const int splits = choose_splits(tiles, K, G, need, WBITS == 8 || XD == LQ_BF16);
+  const int splits = choose_splits(tiles, K, G, need, WBITS == 8 || XD != LQ_F16);
   if (splits > 1) {
     const int rc = launch_gemm_split<GemmSmall, WBITS, SD, OD, EPI, XD>(X, W, S, O, M, N, K, G,
                                                                         splits, st, fixed, sd_rt, od_rt);
@@ -1334,6 +1345,20 @@ int launch_gemm_x(const void* X, const void* W, const void* S, void* O, int64_t 
   if (xd != LQ_BF16 || G % (kBK / 2) != 0) return LQ_ERR_SHAPE;
   return launch_gemm_t<WBITS, kRT, kRT, false, LQ_BF16>(X, W, S, O, M, N, K, G, st, fixed, sd, od);
 }
+// fp32 activations as bf16 part rows P [2 M, K] (rows 2i, 2i + 1 = the two
+// parts of row i): the bf16 GEMM on 2 M rows with the pair sum in its
+// epilogue, O [M, N] (od).  M2 = 2 M.
+template <int WBITS>
+int launch_gemm_f32_parts(const void* P, const void* W, const void* S, void* O, int64_t M2,
+                          int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  if (M2 % 2 != 0 || G % (kBK / 2) != 0 || K % kBK != 0) return LQ_ERR_SHAPE;
+  return launch_gemm_t<WBITS, kRT, kRT, false, LQ_F32>(P, W, S, O, M2, N, K, G, st, nullptr, sd, od);
+}
+template int launch_gemm_f32_parts<4>(const void*, const void*, const void*, void*, int64_t,
+                                      int64_t, int64_t, int64_t, int, int, hipStream_t);
+template int launch_gemm_f32_parts<8>(const void*, const void*, const void*, void*, int64_t,
+                                      int64_t, int64_t, int64_t, int, int, hipStream_t);
+
 template int launch_gemm_x<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
                               int64_t, int64_t, int, int, int, hipStream_t, const FixedScratch*);
 template int launch_gemm_x<8>(const void*, const void*, const void*, void*, int64_t, int64_t,

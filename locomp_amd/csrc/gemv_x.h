@@ -8,16 +8,16 @@ namespace lq {
 
 void* stream_workspace(int slot, size_t bytes, hipStream_t st);
 
-// fp32 activations X [M, K] -> their bf16 parts, P bf16 with row m + pstride
-// * part = part `part` of row m: NPARTS = 3, the exact three-way split (the
-// tile kernel's 12 part rows at M <= 4, pstride 4: rows of m >= M are not
-// written and not read); NPARTS = 2, the round-to-nearest two-way split (the
-// stacked [2 M, K] layout, pstride M).  Thread i takes 8 consecutive k of one
-// row.
+// fp32 activations X [M, K] -> their bf16 parts, P bf16 with row m * mstride
+// + pstride * part = part `part` of row m: NPARTS = 3, the exact three-way
+// split (the tile kernel's 12 part rows at M <= 4: mstride 1, pstride 4; rows
+// of m >= M are not written and not read); NPARTS = 2, the round-to-nearest
+// two-way split (rows 2m, 2m + 1: mstride 2, pstride 1).  Thread i takes 8
+// consecutive k of one row.
 template <int NPARTS>
 static __global__ __launch_bounds__(256) void split_f32_parts_kernel(const float* __restrict__ X,
                                                              uint16_t* __restrict__ P, int M,
-                                                             int K, int pstride) {
+                                                             int K, int mstride, int pstride) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int per_row = K >> 3;
   if (i >= M * per_row) return;
@@ -33,18 +33,19 @@ static __global__ __launch_bounds__(256) void split_f32_parts_kernel(const float
       h[e] = (NPARTS == 3 ? f32_part_bits(x[e], p) : f32_rn2_part_bits(x[e], p)) >> 16;
     const u32x4_t v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
                        h[6] | (h[7] << 16)};
-    *reinterpret_cast<u32x4_t*>(P + (size_t(m) + size_t(pstride) * p) * K + k) = v;
+    *reinterpret_cast<u32x4_t*>(P + (size_t(m) * mstride + size_t(pstride) * p) * K + k) = v;
   }
 }
 
-// O [M, N] = P[0] + P[1] (the two part rows' fp32 products, [2, M, N], added in
-// that order), stored as od.
+// O [M, N] = P[2m] + P[2m + 1] (the two part rows' fp32 products, [2 M, N],
+// added in that order), stored as od.
 static __global__ __launch_bounds__(256) void sum_part_rows_kernel(const float* __restrict__ P,
                                                            void* __restrict__ O, int64_t MN,
-                                                           int od) {
+                                                           int N, int od) {
   const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (e >= MN) return;
-  store_out<kRT>(O, size_t(e), P[e] + P[MN + e], od);
+  const int64_t m = e / N, at = e + m * N;   // 2 m N + n
+  store_out<kRT>(O, size_t(e), P[at] + P[at + N], od);
 }
 
 template <int WBITS, int XD, int NSC>
@@ -239,7 +240,7 @@ int launch_skinny_x(const void* X, const void* W, const void* S, void* O, int64_
   if (parts) {
     const int threads = int(M * (K / 8));
     hipLaunchKernelGGL(split_f32_parts_kernel<3>, dim3((threads + 255) / 256), dim3(256), 0, st,
-                       static_cast<const float*>(X), static_cast<uint16_t*>(parts), int(M), int(K), 4);
+                       static_cast<const float*>(X), static_cast<uint16_t*>(parts), int(M), int(K), 1, 4);
     X = parts;
     LQ_NSC(kXPre)
   } else if (xd == LQ_BF16) {

@@ -4,19 +4,20 @@
 namespace lq {
 
 // fp32 rows X [M, K] (K % 8 == 0) -> their round-to-nearest bf16 parts
-// P [2 M, K], row p M + m = part p of row m.
+// P [2 M, K], row 2 m + p = part p of row m.
 int launch_split_f32_rows(const float* X, void* P, int64_t M, int64_t K, hipStream_t st) {
   const int64_t threads = M * (K / 8);
   hipLaunchKernelGGL(split_f32_parts_kernel<2>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, st,
-                     X, static_cast<uint16_t*>(P), int(M), int(K), int(M));
+                     X, static_cast<uint16_t*>(P), int(M), int(K), 2, 1);
   return check_launch();
 }
 
-// O [M, N] (od) = sum of the two part rows' products P [2, M, N] (fp32).
+// O [M, N] (od) = sum of the two part rows' products P [2 M, N] (fp32, rows
+// 2 m and 2 m + 1).
 int launch_sum_part_rows(const float* P, void* O, int64_t M, int64_t N, int od, hipStream_t st) {
   const int64_t mn = M * N;
   hipLaunchKernelGGL(sum_part_rows_kernel, dim3(unsigned((mn + 255) / 256)), dim3(256), 0, st, P, O,
-                     mn, od);
+                     mn, int(N), od);
   return check_launch();
 }
 

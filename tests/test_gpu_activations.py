@@ -3,7 +3,9 @@ fp32 `locomp.Tensor` activations, examples/38_quantized_matmul.py:30-40, and
 its frontend types bf16 parameters as locomp.BFloat16, locomp/frontend.py:53).
 
 Both run on bf16 MFMAs with exact integer weights and fp32 group scales:
-bf16 activations as given, fp32 ones split exactly into three bf16 parts.
+bf16 activations as given, fp32 ones split into bf16 parts: three exact
+parts on the row and tile kernels (M <= 4), two round-to-nearest parts
+(residual <= 2^-16 |x|) on the M = 1 segment kernel and beyond four rows.
 The oracle is the restated reference NumPy path on the same values (bf16
 activations widened exactly to fp32).  Bars: rtol / atol 1e-2 for bf16
 activations; rtol 1e-4 (+ atol 1e-5 max|Y|) for fp32.
@@ -179,9 +181,11 @@ def test_fp32_activations_shapes(wbits, M, N, K, G, sd):
     (4, 16, 576, 576, 32, "f16"),       # < 2^24 multiply-adds: the generic kernel
 ])
 def test_fp32_activations_beyond_four_rows(wbits, M, N, K, G, sd):
-    """fp32 activations at M > 4: exact bf16 parts stacked as 3 M rows on the
-    bf16 route (tile kernel or MFMA GEMM) with fp32 products, the three part
-    rows added; full output against the oracle at rtol 1e-4."""
+    """fp32 activations at M > 4: two round-to-nearest bf16 parts per row as
+    2 M rows on the bf16 route: the tile kernels with fp32 products and a
+    second launch adding the part rows (2 M <= 64), else the MFMA GEMM adding
+    them in its epilogue (M = 40: k split, partial sums of the pair sums);
+    full output against the oracle at rtol 1e-4."""
     X, W, S = _case(wbits, M, N, K, G, seed=M + N + K + wbits)
     X = X * np.float32(3.0)
     got = _run(wbits, X, W, S, N, K, G, "f32", sd, "f32")
@@ -273,14 +277,15 @@ def test_fp32_split_is_exact_on_hard_values_m3():
 
 @pytest.mark.parametrize("M", [8, 64])
 def test_fp32_stacked_route_tiny_and_mixed_magnitudes(M):
-    """fp32 activations beyond four rows run as three bf16 part rows each
-    (x = hi + mid + lo) on the bf16 MFMA route, whose fp32 part-row products
-    are added as (P0 + P1) + P2.  Even rows hold activations of magnitude
-    ~1e-36, whose mid and lo parts lie below bf16's normal range (2^-126);
-    odd rows spread over 2^-30 .. 2^30 within the row.  Against the generic
-    fp32 kernel (one fp32 FMA chain per output) and a float64 oracle, each
-    output stays within 2e-5 of sum_k |x_k w_nk| of its row: a flushed mid
-    part would err by up to 2^-8 of the tiny rows' terms."""
+    """fp32 activations beyond four rows run as two bf16 part rows each
+    (hi = RN(x), lo = RN(x - hi)) on the bf16 MFMA route (M = 8: tile kernel,
+    products added by a second launch; M = 64: the GEMM, added in its
+    epilogue).  Even rows hold activations of magnitude ~1e-36, whose lo
+    parts lie below bf16's normal range (2^-126); odd rows spread over
+    2^-30 .. 2^30 within the row.  Against the generic fp32 kernel (one fp32
+    FMA chain per output) and a float64 oracle, each output stays within
+    2e-5 of sum_k |x_k w_nk| of its row: a flushed lo part would err by up
+    to 2^-9 of the tiny rows' terms."""
     rng = np.random.default_rng(40 + M)
     N, K, G = 2048, 2048, 32
     X = rng.standard_normal((M, K)).astype(np.float32)
@@ -349,12 +354,13 @@ def test_fp32_activations_in_graph_on_a_fresh_stream():
         _close32(Oe.cpu().numpy(), want)
 
 
-def test_fp32_activations_beyond_four_rows_in_graph():
-    """fp32 at M > 4 needs two workspaces (part rows, fp32 products): a
-    capture on a stream that has none takes the generic kernel; after an
-    eager call on the same stream the capture takes the split route.  Both
-    graphs are replayed three times with eager work in between, every result
-    against the oracle."""
+@pytest.mark.parametrize("M", [8, 40])
+def test_fp32_activations_beyond_four_rows_in_graph(M):
+    """fp32 at M > 4 needs workspaces (part rows; at M = 8 the fp32 products,
+    at M = 40 the GEMM's split-K partial sums): a capture on a stream that
+    has none takes the generic kernel; after an eager call on the same stream
+    the capture takes the split route.  Both graphs are replayed three times
+    with eager work in between, every result against the oracle."""
     import ctypes
 
     import torch
@@ -363,8 +369,8 @@ def test_fp32_activations_beyond_four_rows_in_graph():
 
     lib = _lib.load()
     vp = ctypes.c_void_p
-    M, N, K, G = 8, 2048, 1024, 128
-    X, W, S = _case(4, M, N, K, G, seed=78)
+    N, K, G = 2048, 1024, 128
+    X, W, S = _case(4, M, N, K, G, seed=78 + M)
     want = _oracle(4, X, W, S, G)
     Xd, Wd, Sd = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (X, W, S))
     Oe = torch.zeros((M, N), dtype=torch.float32, device="cuda")
