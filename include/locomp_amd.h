@@ -200,9 +200,11 @@ int locomp_amd_dequant_matvec_int8(const void* X, const void* W,
  * Replaces two dequant_matvec_int4 launches plus silu_mul_kernel
  * (examples/54_smollm2_inference.py:113-120, 545-548); arguments as
  * locomp_amd_dequant_matvec_int4 with I = intermediate size (half the rows).
- * One launch where a fused kernel covers the shape; otherwise the matvec is
- * staged in an fp32 per-(device, stream) buffer held until the process ends
- * (M x 2I x 4 bytes) and an epilogue kernel follows. */
+ * One launch where a fused kernel covers the shape (fp32 activations: a
+ * split into two bf16 part rows per row, in the stream's workspace, then
+ * one fused launch); otherwise the matvec is staged in an fp32
+ * per-(device, stream) buffer held until the process ends (M x 2I x 4
+ * bytes) and an epilogue kernel follows. */
 int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const void* scales,
                                             void* O, int64_t K_dim, int64_t HALF_K,
                                             int64_t NUM_SCALES, int64_t GROUP_SIZE, int64_t I,

@@ -17,9 +17,14 @@ int launch_skinny(const void*, const void*, const void*, void*, int64_t, int64_t
 template <int WBITS>
 int launch_gemm_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
                   int, int, int, hipStream_t, const FixedScratch*);
-template <int WBITS>
-int launch_gemm_f32_parts(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
-                          int64_t, int, int, hipStream_t);
+template <int WBITS, bool EPI>
+int launch_gemm_pairs(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                      int64_t, int, int, hipStream_t);
+template <int WBITS, int XD, bool EPI>
+int launch_tile_rows_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                       int64_t, int, int, hipStream_t);
+int launch_gemm_silu_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                       int64_t, int, int, hipStream_t);
 template <int WBITS>
 int launch_skinny_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                     int64_t, int, int, int, hipStream_t, const FixedScratch*);
@@ -39,7 +44,6 @@ int launch_zero_fill(void*, int64_t, int, hipStream_t);
 int launch_split_f32_rows(const float*, void*, int64_t, int64_t, hipStream_t);
 int launch_rows_silu_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                        int64_t, int, int, int, hipStream_t);
-int launch_sum_part_rows(const float*, void*, int64_t, int64_t, int, hipStream_t);
 int launch_rms_norm(void*, const void*, const void*, void*, int64_t, int64_t, float, int,
                     hipStream_t);
 int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
@@ -81,53 +85,44 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
                            int64_t G, int64_t N, int64_t M, int xd, int sd, int od, hipStream_t st,
                            const FixedScratch* fixed = nullptr);
 
-// fp32 activations at M > 4: each row split into two bf16 parts with round
-// to nearest (hi = RN(x), lo = RN(x - hi): |x - hi - lo| <= 2^-16 |x|),
-// as 2 M bf16 rows in the stream's workspace slot 2 (row 2i + p = part p of
-// row i) and run through the bf16 route: the MFMA GEMM adds the two part
-// rows' products in its epilogue (2 M > 64); the decode kernels write them
-// as fp32 (slot 3) and a second launch adds them.  Each part times an integer weight is exact in fp32, so the result
-// differs from an fp32 dot product by at most 2^-16 sum_k |x_k w_nk| beyond
-// the summation order: no more than fp32 accumulation's own worst case
-// (K 2^-24 sum_k |x_k w_nk|) for K >= 256.  Taken only where the bf16 route
-// is a fast one (2 M <= 16: the tile kernel; else the MFMA GEMM, G % 32),
-// in row blocks whose buffers fit the workspace cap; LQ_ERR_SHAPE (the
-// caller falls back) when it does not apply or a workspace is missing (a
-// capture on a stream that has none yet).
-template <int WBITS>
-static int matmul_f32_stacked(const void* X, const void* W, const void* S, void* O, int64_t K,
-                              int64_t G, int64_t N, int64_t M, int sd, int od, hipStream_t st) {
-  if (2 * M > 16 && (G % 32 != 0 || K % 64 != 0)) return LQ_ERR_SHAPE;
-  // below ~2^24 multiply-adds its three launches cost more than the generic
+// fp32 activations at M > 4 (and gate|up beyond the row kernel): each row
+// split into two bf16 parts with round to nearest (hi = RN(x), lo = RN(x -
+// hi): |x - hi - lo| <= 2^-16 |x|), as 2 M bf16 rows in the stream's
+// workspace slot 2 (row 2i + p = part p of row i), run on the bf16 kernels:
+// the decode kernels for 2 M <= 64, else the MFMA GEMM (G % 32), whose
+// stores add each row's two part products (EPI: then silu(gate) * up of the
+// interleaved gate/up rows, O [M, N / 2]).  Each part times an integer
+// weight is exact in fp32, so the result differs from an fp32 dot product by
+// at most 2^-16 sum_k |x_k w_nk| beyond the summation order: no more than
+// fp32 accumulation's own worst case (K 2^-24 sum_k |x_k w_nk|) for
+// K >= 256.  Row blocks keep the part rows within the workspace cap.
+// LQ_ERR_SHAPE (the caller falls back; it rewrites every row) when no fast
+// kernel takes the shape or the workspace is missing (a capture on a stream
+// that has none yet).
+template <int WBITS, bool EPI>
+static int f32_pair_rows(const void* X, const void* W, const void* S, void* O, int64_t K,
+                         int64_t G, int64_t N, int64_t M, int sd, int od, hipStream_t st) {
+  // below ~2^24 multiply-adds its two launches cost more than the generic
   // kernel (16 x 576 x 576 with three parts: 20 us against 11)
   if (M * N * K < (int64_t(1) << 24)) return LQ_ERR_SHAPE;
   constexpr int64_t kCap = int64_t(256) << 20;          // bytes per workspace slot
-  const int64_t rows = std::max<int64_t>(1, std::min(kCap / (2 * K * 2), kCap / (2 * N * 4)));
-  const int64_t mb = std::min(M, rows);
+  const int64_t mb = std::min(M, std::max<int64_t>(1, kCap / (2 * K * 2)));
   void* parts = stream_workspace(2, size_t(2 * mb * K * 2), st);
   if (parts == nullptr) return LQ_ERR_SHAPE;
-  const size_t osz = od == LQ_F32 ? 4 : 2;
+  const size_t orow = size_t(EPI ? N / 2 : N) * (od == LQ_F32 ? 4 : 2);
+  // few long rows at N = 4096-class widths: the split-K GEMM beats the
+  // activation-in-LDS kernel, as for bf16 activations
+  const bool gemm_first = N > 3072 && N <= 4096 && K >= 10240;
   for (int64_t m0 = 0; m0 < M; m0 += mb) {
     const int64_t m = std::min(mb, M - m0);
-    uint8_t* out = static_cast<uint8_t*>(O) + size_t(m0 * N) * osz;
+    uint8_t* out = static_cast<uint8_t*>(O) + size_t(m0) * orow;
     int rc = launch_split_f32_rows(static_cast<const float*>(X) + m0 * K, parts, m, K, st);
     if (rc != LQ_OK) return rc;
-    if (2 * m > 64) {
-      // the bf16 GEMM adds each row's two part products in its epilogue
-      rc = launch_gemm_f32_parts<WBITS>(parts, W, S, out, 2 * m, N, K, G, sd, od, st);
-      if (rc != LQ_ERR_SHAPE) {
-        if (rc != LQ_OK) return rc;
-        continue;
-      }
-    }
-    // decode-sized blocks (and a GEMM without its split workspace): the
-    // bf16 route into fp32 products, then the pair sum
-    // (without it the caller's fallback rewrites every row)
-    void* prod = stream_workspace(3, size_t(2 * mb * N * 4), st);
-    if (prod == nullptr) return LQ_ERR_SHAPE;
-    rc = matmul_dispatch<WBITS>(parts, W, S, prod, K, G, N, 2 * m, LQ_BF16, sd, LQ_F32, st);
-    if (rc != LQ_OK) return rc;
-    rc = launch_sum_part_rows(static_cast<const float*>(prod), out, m, N, od, st);
+    rc = LQ_ERR_SHAPE;
+    if (2 * m <= 64 && !(2 * m > 16 && gemm_first))
+      rc = launch_tile_rows_x<WBITS, kXPairs, EPI>(parts, W, S, out, 2 * m, N, K, G, sd, od, st);
+    if (rc == LQ_ERR_SHAPE)
+      rc = launch_gemm_pairs<WBITS, EPI>(parts, W, S, out, 2 * m, N, K, G, sd, od, st);
     if (rc != LQ_OK) return rc;
   }
   return LQ_OK;
@@ -159,7 +154,7 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
   }
   if (fast_common && xd == LQ_F32 && M > 4 && fixed == nullptr) {
     // fp32 beyond the decode kernels' 4 rows: two bf16 parts on the bf16 route
-    const int rc = matmul_f32_stacked<WBITS>(X, W, S, O, K, G, N, M, sd, od, st);
+    const int rc = f32_pair_rows<WBITS, false>(X, W, S, O, K, G, N, M, sd, od, st);
     if (rc != LQ_ERR_SHAPE) return rc;
   }
   if (fast_common && xd == LQ_BF16 && M > 16 && M <= 64 &&
@@ -328,9 +323,11 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
   const int64_t N = 2 * I;
   const bool fast = fast_allowed() && aligned(X, 16) && aligned(W, 16) && aligned(scales, 4) &&
                     M * K_dim <= kMax32 && N * HALF_K <= kMax32 && N * NUM_SCALES <= kMax32;
-  // the fused epilogues are instantiated for fp16 activations with fp16 /
-  // fp32 scales and outputs; bf16 ones and bf16 / fp32 activations take the
-  // staged path below (fast matvec, then the pairwise epilogue)
+  // the fp16 fused epilogues are instantiated for fp16 / fp32 scales and
+  // outputs; bf16 / fp32 activations have their own (any of the three
+  // scale / output dtypes); fp16 activations with bf16 scales or outputs,
+  // and shapes no fused kernel takes, take the staged path below (fast
+  // matvec, then the pairwise epilogue)
   const bool fused = x_dtype == LQ_F16 && scale_dtype != LQ_BF16 && out_dtype != LQ_BF16;
   if (fast) {
     rc = LQ_ERR_SHAPE;
@@ -339,9 +336,22 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
     else if (fused)
       rc = launch_silu_fast(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
     if (rc != LQ_ERR_SHAPE) return rc;
-    if (!fused && K_dim % 8 == 0)   // bf16 / fp32 activations or bf16 dtypes, M <= 2: the row kernel
+    if (!fused && K_dim % 8 == 0) {
+      // bf16 / fp32 activations or bf16 dtypes, M <= 2: the row kernel
       rc = launch_rows_silu_x(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
                               out_dtype, st);
+      // bf16 activations: the decode kernels (M <= 64), else the MFMA GEMM
+      if (rc == LQ_ERR_SHAPE && x_dtype == LQ_BF16 && M <= 64)
+        rc = launch_tile_rows_x<4, LQ_BF16, true>(X, W, scales, O, M, N, K_dim, GROUP_SIZE,
+                                                  scale_dtype, out_dtype, st);
+      if (rc == LQ_ERR_SHAPE && x_dtype == LQ_BF16)
+        rc = launch_gemm_silu_x(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype,
+                                st);
+      // fp32 activations: their two bf16 part rows on the same kernels
+      if (rc == LQ_ERR_SHAPE && x_dtype == LQ_F32)
+        rc = f32_pair_rows<4, true>(X, W, scales, O, K_dim, GROUP_SIZE, N, M, scale_dtype,
+                                    out_dtype, st);
+    }
     if (rc != LQ_ERR_SHAPE) return rc;
     // No fused kernel for this shape: the fast matvec into an fp32 staging
     // buffer (slot 1 of the stream's workspace), then the pairwise epilogue.

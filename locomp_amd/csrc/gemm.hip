@@ -124,10 +124,11 @@ __device__ __forceinline__ void xcd_tile(int b, int tiles_m, int tiles_n, int a_
 // O [M, N / 2] (columns n and n + 1 sit in lanes r16 and r16 ^ 1).
 // XD: activation dtype, fp16 (fp16 MFMA) or bf16 (bf16 MFMA; B holds the
 // exact integers q - 8 / q as bf16 and the scales are applied in fp32, like
-// int8).  XD = LQ_F32: bf16 part rows of fp32 activations, the two parts of
+// int8).  XD = kXPairs: bf16 part rows of fp32 activations, the two parts of
 // row i at rows 2i and 2i + 1 (M counts part rows); the epilogue adds each
-// pair (rows 4 q + r and 4 q + r + 1 sit in one lane) and stores O [M / 2, N].
-// SD / OD = kRT take the scale / output dtype from sd_rt / od_rt.
+// pair (rows 4 q + r and 4 q + r + 1 sit in one lane) and stores O [M / 2, N]
+// (EPI: [M / 2, N / 2]).  SD / OD = kRT take the scale / output dtype from
+// sd_rt / od_rt.
 template <class C, int WBITS, int SD, int OD, bool EPI = false, int XD = LQ_F16>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     const half_t* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
@@ -135,9 +136,8 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
     int kspan, int sd_rt = 0, int od_rt = 0) {
   constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN;
   static_assert(BM % (8 * C::kWaves) == 0, "A DMA: whole 1 KB instructions per wave");
-  constexpr bool kParts = XD == LQ_F32;
+  constexpr bool kParts = XD == kXPairs;
   constexpr bool kBf = XD == LQ_BF16 || kParts;
-  static_assert(!(kParts && EPI), "part rows take the plain epilogue");
   typedef typename Elem<SD == kRT ? LQ_F32 : SD>::T stype;
   __shared__ __attribute__((aligned(16))) half_t As[kAStages][BM * kBK];
   __shared__ __attribute__((aligned(16))) half_t Bs[kBStages][BN * kBK];
@@ -486,16 +486,22 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_w4_kernel(
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int n = n0 + (wn * TN + j) * 16 + r16;
-        if constexpr (EPI) {
+        if constexpr (kParts) {
+          // hi part + lo part (M even: row m + 1 < M with m)
+          if ((r & 1) != 0) continue;
+          const float y = acc[i][j][r] + acc[i][j][(r + 1) & 3];
+          if constexpr (EPI) {
+            const float up = __shfl_xor(y, 1, 64);
+            if ((r16 & 1) == 0 && m < M && n < N)
+              store_out<OD>(O, size_t(m >> 1) * (N / 2) + n / 2, y / (1.0f + expf(-y)) * up, od_rt);
+          } else {
+            if (m < M && n < N) store_out<OD>(O, obase + size_t(m >> 1) * N + n, y, od_rt);
+          }
+        } else if constexpr (EPI) {
           const float g = acc[i][j][r];
           const float up = __shfl_xor(g, 1, 64);
           if ((r16 & 1) == 0 && m < M && n < N)
             store_out<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up, od_rt);
-        } else if constexpr (kParts) {
-          // hi part + lo part (M even: row m + 1 < M with m)
-          if ((r & 1) == 0 && m < M && n < N)
-            store_out<OD>(O, obase + size_t(m >> 1) * N + n, acc[i][j][r] + acc[i][j][r + 1],
-                          od_rt);
         } else {
           if (m < M && n < N) store_out<OD>(O, obase + size_t(m) * N + n, acc[i][j][r], od_rt);
         }
@@ -1139,7 +1145,8 @@ static int min_splits(int64_t K, int64_t G) {
 template <int OD>
 __global__ __launch_bounds__(256) void split_reduce_silu_kernel(const float* __restrict__ P,
                                                                 void* __restrict__ O, int64_t M,
-                                                                int64_t N, int splits) {
+                                                                int64_t N, int splits,
+                                                                int od_rt = 0) {
   const int64_t half = N / 2;
   const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (e >= M * half) return;
@@ -1151,7 +1158,7 @@ __global__ __launch_bounds__(256) void split_reduce_silu_kernel(const float* __r
     g += P[size_t(s) * mn + at];
     u += P[size_t(s) * mn + at + 1];
   }
-  store_f32<OD>(O, size_t(e), g / (1.0f + expf(-g)) * u);
+  store_out<OD>(O, size_t(e), g / (1.0f + expf(-g)) * u, od_rt);
 }
 
 // Number of k splits for `tiles` output tiles: the largest of 8, 6, 4, 3, 2
@@ -1187,7 +1194,7 @@ static int launch_gemm_split(const void* X, const void* W, const void* S, void* 
                              int64_t N, int64_t K, int64_t G, int splits, hipStream_t st,
                              const FixedScratch* fixed, int sd_rt = 0, int od_rt = 0) {
   // (part rows: the reduction sees the summed rows)
-  const size_t mn = size_t(XD == LQ_F32 ? M / 2 : M) * size_t(N);
+  const size_t mn = size_t(XD == kXPairs ? M / 2 : M) * size_t(N);
   const size_t ws_bytes = mn * sizeof(float) * size_t(splits);
   void* ws;
   if (fixed != nullptr) {   // caller-provided scratch: never allocate
@@ -1202,7 +1209,8 @@ static int launch_gemm_split(const void* X, const void* W, const void* S, void* 
   if (rc != LQ_OK) return rc;
   if constexpr (EPI)
     hipLaunchKernelGGL((split_reduce_silu_kernel<OD>), dim3(unsigned((mn / 2 + 255) / 256)), dim3(256),
-                       0, st, static_cast<const float*>(ws), O, M, N, splits);
+                       0, st, static_cast<const float*>(ws), O, int64_t(mn / size_t(N)), N, splits,
+                       od_rt);
   else
     hipLaunchKernelGGL((split_reduce_kernel<OD>), dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, st,
                        static_cast<const float*>(ws), O, mn, splits, od_rt);
@@ -1347,17 +1355,28 @@ int launch_gemm_x(const void* X, const void* W, const void* S, void* O, int64_t 
 }
 // fp32 activations as bf16 part rows P [2 M, K] (rows 2i, 2i + 1 = the two
 // parts of row i): the bf16 GEMM on 2 M rows with the pair sum in its
-// epilogue, O [M, N] (od).  M2 = 2 M.
-template <int WBITS>
-int launch_gemm_f32_parts(const void* P, const void* W, const void* S, void* O, int64_t M2,
-                          int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+// epilogue, O [M, N] (od; EPI: gate/up rows interleaved, O [M, N / 2]).
+// M2 = 2 M.
+template <int WBITS, bool EPI>
+int launch_gemm_pairs(const void* P, const void* W, const void* S, void* O, int64_t M2, int64_t N,
+                      int64_t K, int64_t G, int sd, int od, hipStream_t st) {
   if (M2 % 2 != 0 || G % (kBK / 2) != 0 || K % kBK != 0) return LQ_ERR_SHAPE;
-  return launch_gemm_t<WBITS, kRT, kRT, false, LQ_F32>(P, W, S, O, M2, N, K, G, st, nullptr, sd, od);
+  return launch_gemm_t<WBITS, kRT, kRT, EPI, kXPairs>(P, W, S, O, M2, N, K, G, st, nullptr, sd, od);
 }
-template int launch_gemm_f32_parts<4>(const void*, const void*, const void*, void*, int64_t,
-                                      int64_t, int64_t, int64_t, int, int, hipStream_t);
-template int launch_gemm_f32_parts<8>(const void*, const void*, const void*, void*, int64_t,
-                                      int64_t, int64_t, int64_t, int, int, hipStream_t);
+template int launch_gemm_pairs<4, false>(const void*, const void*, const void*, void*, int64_t,
+                                         int64_t, int64_t, int64_t, int, int, hipStream_t);
+template int launch_gemm_pairs<8, false>(const void*, const void*, const void*, void*, int64_t,
+                                         int64_t, int64_t, int64_t, int, int, hipStream_t);
+template int launch_gemm_pairs<4, true>(const void*, const void*, const void*, void*, int64_t,
+                                        int64_t, int64_t, int64_t, int, int, hipStream_t);
+
+// Gate|up prefill with bf16 activations and the SiLU * mul epilogue (int4,
+// N = 2 I interleaved rows; scale / output dtypes at run time).
+int launch_gemm_silu_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                       int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  if (G % (kBK / 2) != 0 || K % kBK != 0) return LQ_ERR_SHAPE;
+  return launch_gemm_t<4, kRT, kRT, true, LQ_BF16>(X, W, S, O, M, N, K, G, st, nullptr, sd, od);
+}
 
 template int launch_gemm_x<4>(const void*, const void*, const void*, void*, int64_t, int64_t,
                               int64_t, int64_t, int, int, int, hipStream_t, const FixedScratch*);

@@ -50,7 +50,8 @@ __device__ __forceinline__ void dma16_buf(i32x4_t rsrc, uint32_t voff, const voi
 // O [M, N / 2] instead of O [M, N].
 // XD = activation dtype (fp16, bf16, or fp32 for M <= 4: MFMA row
 // m + 4 part holds part `part` of activation row m; kXPre: the same rows
-// read as bf16 from a matrix of parts split beforehand); SD / OD = kRT take
+// read as bf16 from a matrix of parts split beforehand; kXPairs: M bf16 part
+// rows, pairs 2i, 2i + 1 added into output row i); SD / OD = kRT take
 // the scale / output dtype from sd_rt / od_rt.
 template <int WBITS, int NSC, int TILES, int SD, int OD, bool PART, bool EPI = false,
           int XD = LQ_F16>
@@ -59,7 +60,8 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
     int od_rt = 0) {
   constexpr bool kPre = XD == kXPre;                     // pre-split fp32: bf16 part rows
-  typedef TileMfma<WBITS, kPre ? LQ_BF16 : XD> Mf;
+  constexpr bool kPairs = XD == kXPairs;                 // bf16 part rows 2i, 2i + 1
+  typedef TileMfma<WBITS, (kPre || kPairs) ? LQ_BF16 : XD> Mf;
   typedef typename Mf::op_t op_t;
   typedef typename Mf::x_t x_t;
   const float rgroup = 1.0f / float(group);             // for div_rcp (K < 2^22)
@@ -301,10 +303,24 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_kernel(
       // m of lanes r16, r16 + 16, r16 + 32
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] += __shfl(v[r], lane + 16, 64) + __shfl(v[r], lane + 32, 64);
+      static_assert(!EPI, "three-part fp32 rows take the plain store");
       if (q4 == 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (r < M && n < N) store_out<OD>(O, size_t(r) * N + n, v[r], od_rt);
+      }
+    } else if constexpr (kPairs) {
+#pragma unroll
+      for (int r = 0; r < 4; r += 2) {
+        const int m = q4 * 4 + r;   // part rows m, m + 1: output row m / 2
+        const float y = v[r] + v[r + 1];
+        if constexpr (EPI) {
+          const float up = __shfl_xor(y, 1, 64);
+          if ((r16 & 1) == 0 && m < M && n < N)
+            store_out<OD>(O, size_t(m >> 1) * (N / 2) + n / 2, y / (1.0f + expf(-y)) * up, od_rt);
+        } else {
+          if (m < M && n < N) store_out<OD>(O, size_t(m >> 1) * N + n, y, od_rt);
+        }
       }
     } else {
 #pragma unroll
@@ -356,15 +372,17 @@ constexpr int xl_scale_bytes(int wbits, int tiles, int mtiles) {
 }
 
 // EPI: gate/up rows interleaved; store silu(gate) * up to O [M, N / 2].
-// MT: 16-row activation tiles (2 for M <= 32, else 4).
+// MT: 16-row activation tiles (2 for M <= 32, else 4).  XD: fp16, bf16 or
+// kXPairs (bf16 part rows, M of them; O holds M / 2 rows).
 template <int WBITS, int TILES, int SD, int OD, bool EPI = false, int MT = 4, int XD = LQ_F16>
 __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
     int od_rt = 0) {
-  static_assert(XD == LQ_F16 || XD == LQ_BF16, "fp16 or bf16 activations");
+  static_assert(XD == LQ_F16 || XD == LQ_BF16 || XD == kXPairs, "fp16 or bf16 activations");
   constexpr bool kH = XD == LQ_F16;
-  typedef TileMfma<WBITS, XD> Mf;
+  constexpr bool kPairs = XD == kXPairs;   // bf16 part rows 2i, 2i + 1 of fp32 rows
+  typedef TileMfma<WBITS, kH ? LQ_F16 : LQ_BF16> Mf;
   typedef typename Mf::op_t op_t;
   const float rgroup = 1.0f / float(group);             // for div_rcp (K < 2^22)
   constexpr int kRows = 16 * TILES;
@@ -593,15 +611,17 @@ __global__ __launch_bounds__(512, 1) void gemv_tile_xl_kernel(
     for (int w2 = 1; w2 < 8; ++w2) v += red[((w2 * MT + mt) * TILES + t) * 64 + lane];
     const int n = n0 + t * 16 + r16;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < 4; r += kPairs ? 2 : 1) {
       const int m = mt * 16 + q4 * 4 + r;
+      // pairs: part rows m, m + 1 -> output row m / 2
+      const float y = kPairs ? v[r] + v[(r + 1) & 3] : v[r];
+      const int mo = kPairs ? m >> 1 : m;
       if constexpr (EPI) {
-        const float g = v[r];
-        const float up = __shfl_xor(g, 1, 64);
+        const float up = __shfl_xor(y, 1, 64);
         if ((r16 & 1) == 0 && m < M && n < N)
-          store_out<OD>(O, size_t(m) * (N / 2) + n / 2, g / (1.0f + expf(-g)) * up, od_rt);
+          store_out<OD>(O, size_t(mo) * (N / 2) + n / 2, y / (1.0f + expf(-y)) * up, od_rt);
       } else {
-        if (m < M && n < N) store_out<OD>(O, size_t(m) * N + n, v[r], od_rt);
+        if (m < M && n < N) store_out<OD>(O, size_t(mo) * N + n, y, od_rt);
       }
     }
   }

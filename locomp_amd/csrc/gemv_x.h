@@ -37,18 +37,7 @@ static __global__ __launch_bounds__(256) void split_f32_parts_kernel(const float
   }
 }
 
-// O [M, N] = P[2m] + P[2m + 1] (the two part rows' fp32 products, [2 M, N],
-// added in that order), stored as od.
-static __global__ __launch_bounds__(256) void sum_part_rows_kernel(const float* __restrict__ P,
-                                                           void* __restrict__ O, int64_t MN,
-                                                           int N, int od) {
-  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (e >= MN) return;
-  const int64_t m = e / N, at = e + m * N;   // 2 m N + n
-  store_out<kRT>(O, size_t(e), P[at] + P[at + N], od);
-}
-
-template <int WBITS, int XD, int NSC>
+template <int WBITS, int XD, int NSC, bool EPI = false>
 static void launch_tile_x_nsc(const void* X, const void* W, const void* S, void* O, int64_t M,
                               int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
   // fp32 activations hold twice the registers per batch: at most 2 tiles
@@ -61,11 +50,11 @@ static void launch_tile_x_nsc(const void* X, const void* W, const void* S, void*
 #define LQ_TX_LAUNCH(T_)                                                                        \
   do {                                                                                          \
     if (part)                                                                                   \
-      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, kRT, kRT, true, false, XD>),         \
+      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, kRT, kRT, true, EPI, XD>),           \
                          dim3(blocks), dim3(512), 0, st, X, static_cast<const uint8_t*>(W), S, \
                          O, int(M), int(N), int(K), int(K / G), int(G), sd, od);                \
     else                                                                                        \
-      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, kRT, kRT, false, false, XD>),        \
+      hipLaunchKernelGGL((gemv_tile_kernel<WBITS, NSC, T_, kRT, kRT, false, EPI, XD>),          \
                          dim3(blocks), dim3(512), 0, st, X, static_cast<const uint8_t*>(W), S, \
                          O, int(M), int(N), int(K), int(K / G), int(G), sd, od);                \
   } while (0)
@@ -183,18 +172,38 @@ static int launch_rows_x(const void* X, const void* W, const void* S, void* O, i
 // bf16 activations at 16 < M <= 64 (int8 also 8 < M <= 16 with whole-chunk
 // groups, as for fp16) on the activation-in-LDS kernel with bf16 MFMAs;
 // LQ_ERR_SHAPE where it does not apply.
+// bf16 rows on the decode kernels: the LDS-ring tile kernel (M <= 16) or
+// the activation-in-LDS kernel (16 < M <= 64).  XD = LQ_BF16 (activations)
+// or kXPairs (M bf16 part rows of M / 2 fp32 rows, pairs added at the
+// store); EPI: gate/up rows interleaved, silu(gate) * up stored.
+// LQ_ERR_SHAPE for shapes those kernels do not take.
+template <int WBITS, int XD, bool EPI>
+int launch_tile_rows_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
+                       int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  const int ssz = sd == LQ_F32 ? 4 : 2;
+  if (M <= 16) {
+    if (!gemv_tile_ok(WBITS, M, N, K, G, ssz)) return LQ_ERR_SHAPE;
+    const int64_t eighth_k = kTBlocks * TileMfma<WBITS>::kSpan;
+    const int nsc = G >= eighth_k ? 1 : int(eighth_k / G);
+    if (nsc == 1) launch_tile_x_nsc<WBITS, XD, 1, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+    else if (nsc == 2) launch_tile_x_nsc<WBITS, XD, 2, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+    else launch_tile_x_nsc<WBITS, XD, 4, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+    return check_launch();
+  }
+  if (M > 64 || !gemv_tile_xl_ok(WBITS, M, N, K, G, ssz)) return LQ_ERR_SHAPE;
+  if (xl_mtiles(M) <= 2)
+    launch_gemv_tile_xl_mt<WBITS, kRT, kRT, EPI, 2, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+  else
+    launch_gemv_tile_xl_mt<WBITS, kRT, kRT, EPI, 4, XD>(X, W, S, O, M, N, K, G, st, sd, od);
+  return check_launch();
+}
+
+// bf16 activations, 16 < M <= 64.
 template <int WBITS>
 int launch_tile_xl_x(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
                      int64_t K, int64_t G, int sd, int od, hipStream_t st) {
-  if (!gemv_tile_xl_ok(WBITS, M, N, K, G, sd == LQ_F32 ? 4 : 2)) return LQ_ERR_SHAPE;
-  const int mt = xl_mtiles(M);
-  if (mt == 1 && WBITS == 8)
-    launch_gemv_tile_xl_mt<WBITS, kRT, kRT, false, 1, LQ_BF16>(X, W, S, O, M, N, K, G, st, sd, od);
-  else if (mt <= 2)
-    launch_gemv_tile_xl_mt<WBITS, kRT, kRT, false, 2, LQ_BF16>(X, W, S, O, M, N, K, G, st, sd, od);
-  else
-    launch_gemv_tile_xl_mt<WBITS, kRT, kRT, false, 4, LQ_BF16>(X, W, S, O, M, N, K, G, st, sd, od);
-  return check_launch();
+  if (M <= 16) return LQ_ERR_SHAPE;
+  return launch_tile_rows_x<WBITS, LQ_BF16, false>(X, W, S, O, M, N, K, G, sd, od, st);
 }
 
 // bf16 activations at M <= 16, fp32 at M <= 4 (three MFMA rows per

@@ -12,17 +12,11 @@ int launch_split_f32_rows(const float* X, void* P, int64_t M, int64_t K, hipStre
   return check_launch();
 }
 
-// O [M, N] (od) = sum of the two part rows' products P [2 M, N] (fp32, rows
-// 2 m and 2 m + 1).
-int launch_sum_part_rows(const float* P, void* O, int64_t M, int64_t N, int od, hipStream_t st) {
-  const int64_t mn = M * N;
-  hipLaunchKernelGGL(sum_part_rows_kernel, dim3(unsigned((mn + 255) / 256)), dim3(256), 0, st, P, O,
-                     mn, int(N), od);
-  return check_launch();
-}
-
 template int launch_tile_xl_x<4>(const void*, const void*, const void*, void*, int64_t,
                                   int64_t, int64_t, int64_t, int, int, hipStream_t);
+template int launch_tile_rows_x<4, kXPairs, false>(const void*, const void*, const void*, void*,
+                                                   int64_t, int64_t, int64_t, int64_t, int, int,
+                                                   hipStream_t);
 // Gate / up rows interleaved with the SiLU * mul epilogue on the row kernel
 // for what the fp16 fused kernels do not take (bf16 / fp32 activations,
 // bf16 scales or outputs), M <= 2 (fp32: M = 1, K <= 4096).

@@ -72,6 +72,12 @@ constexpr int kRT = -1;
 // beforehand into their three exact bf16 parts: a bf16 matrix of 12 rows,
 // row m + 4 part = part `part` of activation row m (M <= 4).
 constexpr int kXPre = 100;
+// Activation code of the decode kernels and the prefill GEMM for fp32
+// activations split beforehand into two round-to-nearest bf16 parts, rows
+// 2i (hi) and 2i + 1 (lo) of a bf16 matrix of 2 M rows (the kernels' M):
+// the MFMA output rows 4q + r and 4q + r + 1 sit in one lane, so the store
+// adds each pair and writes output row i.
+constexpr int kXPairs = 101;
 template <int SD>
 __device__ __forceinline__ int scale_size(int sd_rt) {
   const int sd = SD == kRT ? sd_rt : SD;

@@ -179,6 +179,9 @@ def test_fp32_activations_shapes(wbits, M, N, K, G, sd):
     (4, 8, 2048, 1024, 32, "f16"),      # G = 32: the GEMM scales after each 32-k half
     (8, 40, 600, 1152, 96, "f32"),      # G = 96: groups end mid-step and at step ends
     (4, 16, 576, 576, 32, "f16"),       # < 2^24 multiply-adds: the generic kernel
+    (8, 7, 3000, 4096, 128, "f16"),     # int8, 14 part rows: the tile kernel
+    (8, 20, 1000, 2048, 64, "f32"),     # int8, 40 part rows: the activation-in-LDS kernel
+    (4, 24, 4096, 11008, 128, "f16"),   # 48 part rows, long rows at N = 4096: the split-K GEMM
 ])
 def test_fp32_activations_beyond_four_rows(wbits, M, N, K, G, sd):
     """fp32 activations at M > 4: two round-to-nearest bf16 parts per row as

@@ -605,8 +605,10 @@ def test_matvec_int4_silu_mul(policy, M, I, K, G, xd):
 @pytest.mark.parametrize("xd,sd,od", [("f16", "bf16", "bf16"), ("bf16", "f16", "bf16"),
                                       ("bf16", "bf16", "f32"), ("f32", "f32", "f32")])
 def test_matvec_int4_silu_mul_other_dtypes(M, I, K, G, xd, sd, od):
-    """bf16 scales / outputs and bf16 / fp32 activations: the fast matvec
-    into the staged fp32 buffer, then the pairwise epilogue."""
+    """bf16 scales / outputs and bf16 / fp32 activations: fp16 activations
+    with bf16 dtypes take the fast matvec into the staged fp32 buffer, then
+    the pairwise epilogue; bf16 / fp32 activations the fused epilogues (row
+    kernel, decode kernels, GEMM; fp32 as two bf16 part rows per row)."""
     Xa, Wg, Sg = synth.matvec_case(4, M, I, K, G, 0.01, 0.05, x_dtype=np.float32,
                                    s_dtype=np.float32, seed=I + K + 7)
     _, Wu, Su = synth.matvec_case(4, M, I, K, G, 0.01, 0.05, x_dtype=np.float32,
@@ -623,6 +625,59 @@ def test_matvec_int4_silu_mul_other_dtypes(M, I, K, G, xd, sd, od):
     want, bound = _silu_mul_oracle(Xu, Wg, Sgu, Wu, Suu, G)
     if od == "bf16":
         bound = bound + 2.0 ** -8 * np.abs(want)
+    err = np.abs(got - want)
+    assert (err <= bound).all(), (err.max(), np.argmax(err - bound))
+
+
+@pytest.mark.parametrize("M,I,K,G,xd,sd,od", [
+    (4, 1536, 2048, 32, "bf16", "f32", "f32"),     # tile kernel
+    (3, 1500, 4128, 32, "bf16", "bf16", "f16"),    # tile kernel, partial last chunk
+    (40, 1000, 1024, 128, "bf16", "f16", "bf16"),  # activation-in-LDS kernel
+    (96, 600, 1024, 32, "bf16", "f32", "f32"),     # GEMM, k split
+    (300, 1100, 512, 64, "bf16", "f16", "f16"),    # GEMM, ragged tiles
+    (1, 1536, 6144, 32, "f32", "f32", "f32"),      # 2 part rows, tile kernel (row kernel: K <= 4096)
+    (3, 1536, 2048, 32, "f32", "f32", "f32"),      # 6 part rows, tile kernel
+    (8, 1000, 2048, 64, "f32", "bf16", "f32"),     # 16 part rows
+    (20, 1000, 1024, 128, "f32", "f32", "f16"),    # 40 part rows, activation-in-LDS kernel
+    (40, 600, 2048, 64, "f32", "f32", "f32"),      # 80 part rows, GEMM with k split
+    (300, 1100, 1024, 32, "f32", "f16", "f32"),    # GEMM, ragged tiles
+])
+def test_silu_mul_fused_bf16_fp32_activations(M, I, K, G, xd, sd, od):
+    """The SiLU * mul epilogue on the bf16 MFMA kernels for bf16 activations
+    and for fp32 ones (two round-to-nearest bf16 part rows per row, added at
+    the store before the epilogue).  fp32 outputs of fp32 activations are
+    held to the fp32 bar: |err| <= 1e-4 (1.1 |u| sum|x w_gate| + |silu(g)|
+    sum|x w_up|), the propagated rtol 1e-4 of the gate and up dot products;
+    others to the fp16 / bf16 bar of the fp16 epilogue tests."""
+    Xa, Wg, Sg = synth.matvec_case(4, M, I, K, G, 0.01, 0.05, x_dtype=np.float32,
+                                   s_dtype=np.float32, seed=I + K + 17)
+    _, Wu, Su = synth.matvec_case(4, M, I, K, G, 0.01, 0.05, x_dtype=np.float32,
+                                  s_dtype=np.float32, seed=I + K + 18)
+    used = {"bf16": lambda a: ref.bf16_bits_to_f32(ref.f32_to_bf16_bits(a)).reshape(a.shape),
+            "f16": lambda a: a.astype(np.float16).astype(np.float32), "f32": lambda a: a}
+    Xu, Sgu, Suu = used[xd](Xa), used[sd](Sg), used[sd](Su)
+    W = lq.interleave_gate_up(Wg, Wu)
+    S = lq.interleave_gate_up(Sg, Su)
+    Xg = _up(Xa, "bf16") if xd == "bf16" else _up(Xa)
+    Sdev = _up(S, "bf16") if sd == "bf16" else _up(S.astype(_dtype(sd)))
+    got = lq.gpu_matvec_int4_silu_mul(Xg, W, Sdev, G, out_dtype=_dtype(od))
+    got = (ref.bf16_bits_to_f32(got).reshape(M, I) if od == "bf16" else got).astype(np.float64)
+    want, bound = _silu_mul_oracle(Xu, Wg, Sgu, Wu, Suu, G)
+    if od == "bf16":
+        bound = bound + 2.0 ** -8 * np.abs(want)
+    if xd == "f32" and od == "f32":
+        def deq(Wp, Sp):
+            q = np.empty((Wp.shape[0], K), np.float64)
+            q[:, 0::2] = (Wp & 15).astype(np.float64) - 8
+            q[:, 1::2] = (Wp >> 4).astype(np.float64) - 8
+            return q * np.repeat(Sp.astype(np.float64), G, axis=1)
+        X64 = Xu.astype(np.float64)
+        Dg, Du = deq(Wg, Sgu), deq(Wu, Suu)
+        g, u = X64 @ Dg.T, X64 @ Du.T
+        silu = g / (1.0 + np.exp(-g))
+        want = silu * u
+        bound = 1e-4 * (1.1 * np.abs(u) * (np.abs(X64) @ np.abs(Dg).T) +
+                        np.abs(silu) * (np.abs(X64) @ np.abs(Du).T)) + 1e-12
     err = np.abs(got - want)
     assert (err <= bound).all(), (err.max(), np.argmax(err - bound))
 
