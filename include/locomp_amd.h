@@ -138,13 +138,15 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * except M = 1 with K <= 4096 where the segment kernel does not apply
  * (K < 2048 or G % 128 != 0), which takes fp32 FMAs on the row kernel;
  * fp32 at M > 4 is split into two round-to-nearest parts, 2 M bf16 rows
- * (row 2i + p = part p of row i) that take the bf16 route: 2 M <= 64 the
- * decode kernels with fp32 products, whose two part rows a second launch
- * adds; else the MFMA GEMM (G % 32 == 0), which adds them in its epilogue
- * (error at most 2^-16 sum_k |x_k w_nk| beyond fp32 summation); other fp32
- * shapes, and a capture on a stream without those workspaces, take a
- * generic kernel.  The fast kernels need X and W 16-byte aligned and the
- * scales 4-byte aligned (otherwise a generic kernel runs).
+ * (row 2i + p = part p of row i) that take the bf16 kernels (2 M <= 64 the
+ * decode kernels, else the MFMA GEMM, G % 32 == 0), whose stores add each
+ * row's two part products (error at most 2^-16 sum_k |x_k w_nk| beyond
+ * fp32 summation).  Scale groups G % 32 != 0 (G % 8 == 0; int8 G % 4),
+ * operands aligned to 4 but not 16 bytes, fp32 shapes below 2^24
+ * multiply-adds and a capture on a stream without the part-row workspace
+ * take a VALU kernel with fp32 FMAs (fp16 / bf16: exact dot2 products);
+ * anything else a generic kernel.  The MFMA kernels need X and W 16-byte
+ * aligned and the scales 4-byte aligned.
  * A prefill GEMM with fewer output tiles than CUs splits K and keeps an fp32
  * workspace per (device, stream), allocated on first use and held until the
  * process ends (int4 and int8 alike). */

@@ -20,6 +20,9 @@ int launch_gemm_x(const void*, const void*, const void*, void*, int64_t, int64_t
 template <int WBITS, bool EPI>
 int launch_gemm_pairs(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                       int64_t, int, int, hipStream_t);
+template <int WBITS, bool EPI>
+int launch_group_valu(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                      int64_t, int, int, int, hipStream_t, const FixedScratch*);
 template <int WBITS, int XD, bool EPI>
 int launch_tile_rows_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                        int64_t, int, int, hipStream_t);
@@ -199,6 +202,12 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
       if (rc != LQ_ERR_SHAPE) return rc;
     }
   }
+  if (fast_allowed() && small_enough) {
+    // scale groups the MFMA kernels do not take (G % 32 != 0), unaligned
+    // operands, and what else is left: fp32 FMAs on the VALU kernel
+    const int rc = launch_group_valu<WBITS, false>(X, W, S, O, M, N, K, G, xd, sd, od, st, fixed);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
   return launch_generic<WBITS>(X, W, S, O, M, N, K, G, xd, sd, od, st);
 }
 
@@ -362,6 +371,11 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
       if (rc != LQ_OK) return rc;
       return launch_silu_pairs(static_cast<const float*>(P), O, M, N, out_dtype, st);
     }
+  }
+  if (fast_allowed() && M * K_dim <= kMax32 && N * K_dim <= kMax32 && M * N <= kMax32) {
+    rc = launch_group_valu<4, true>(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
+                                    out_dtype, st, nullptr);
+    if (rc != LQ_ERR_SHAPE) return rc;
   }
   return launch_generic_silu(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
                              out_dtype, st);

@@ -1318,6 +1318,20 @@ template int launch_gemm_split_only<8>(const void*, const void*, const void*, vo
                                        int64_t, int64_t, int64_t, int, int, hipStream_t,
                                        const FixedScratch*);
 
+// O [M, N] (od) = the sum of `splits` fp32 partial slices P [splits][M][N]
+// (silu: O [M, N / 2] = silu(sum[:, 2i]) * sum[:, 2i + 1]).
+int launch_split_reduce(const float* P, void* O, int64_t M, int64_t N, int splits, bool silu,
+                        int od, hipStream_t st) {
+  const size_t mn = size_t(M) * size_t(N);
+  if (silu)
+    hipLaunchKernelGGL((split_reduce_silu_kernel<kRT>), dim3(unsigned((mn / 2 + 255) / 256)), dim3(256),
+                       0, st, P, O, M, N, splits, od);
+  else
+    hipLaunchKernelGGL((split_reduce_kernel<kRT>), dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, st,
+                       P, O, mn, splits, od);
+  return check_launch();
+}
+
 // O [M, N / 2] = silu(P[:, 2i]) * P[:, 2i + 1] for an fp32 matvec result P.
 int launch_silu_pairs(const float* P, void* O, int64_t M, int64_t N, int od, hipStream_t st) {
   const unsigned blocks = unsigned((M * (N / 2) + 255) / 256);
