@@ -505,17 +505,24 @@ def main():
         # ending with the 49152 x 576 LM head; the chained ones run the
         # reference's per-layer order with the RMSNorms and residual adds
         from locomp_amd.stack import DecodeStack
-        for fused, silu, chain, f32 in ((False, False, False, False), (True, False, False, False),
-                                        (True, True, False, False), (True, True, True, False),
-                                        (True, True, True, True)):
-            st = DecodeStack(fused=fused, silu=silu, chain=chain, f32=f32)
+        # (the _fused_norm_residual ones fold the norms and residual adds
+        # into the linears: 4 launches per layer instead of 6)
+        for fused, silu, chain, f32, fn in ((False, False, False, False, False),
+                                            (True, False, False, False, False),
+                                            (True, True, False, False, False),
+                                            (True, True, True, False, False),
+                                            (True, True, True, True, False),
+                                            (True, True, True, False, True),
+                                            (True, True, True, True, True)):
+            st = DecodeStack(fused=fused, silu=silu, chain=chain, f32=f32, fuse_norm=fn)
             per, _ = time_graph(st, 4, 1)
             d = {"us_per_token": round(per * 1e6, 2), "GB_s": round(st.algo_bytes / per / 1e9, 1),
                  "gemvs_per_token": st.gemvs, "launches_per_token": len(st.links),
                  "algorithmic_bytes": st.algo_bytes,
                  "us_per_launch": round(per * 1e6 / len(st.links), 3)}
             name = "smollm2_135m_int4_g32_decode_step" + ("_qkv_gateup_fused" if fused else "") + \
-                ("_silu_epilogue" if silu else "") + ("_chained_rmsnorm_residual" if chain else "") + \
+                ("_silu_epilogue" if silu else "") + \
+                ("_chained_fused_norm_residual" if fn else "_chained_rmsnorm_residual" if chain else "") + \
                 "_lm_head" + ("_fp32_activations" if f32 else "")
             extra[name] = d
             log(name, d)

@@ -64,7 +64,9 @@ enum {
   LQ_ERR_DTYPE = -2,   /* unknown dtype code                          */
   LQ_ERR_NULL = -3,    /* null pointer with a non-empty problem        */
   LQ_ERR_POLICY = -4,  /* unknown kernel policy                        */
-  LQ_ERR_SCRATCH = -5, /* needs more scratch than the fixed buffer holds */
+  LQ_ERR_SCRATCH = -5, /* needs scratch that is not available: more than the
+                          fixed buffer holds, or a workspace that cannot be
+                          allocated during stream capture */
   LQ_ERR_NAME = -6     /* unknown kernel name (locomp_amd_launch)        */
 };
 
@@ -272,10 +274,38 @@ int locomp_amd_stream_read(const void* buf, int64_t bytes, void* sink, void* str
  * examples/54_smollm2_inference.py:40-73 (args X, W, O, N, EPS_X1000 =
  * eps * 1e6; grid (rows,), launched at :488-489) fused with
  * locomp_launch_add_inplace_kernel (:164-167, the residual adds at :538 and
- * :554).  H, R, gamma and Y share one dtype (LQ_F16 or LQ_F32); fp32
- * arithmetic; Y may not alias H or R. */
+ * :554).  H, R, gamma and Y share one dtype (LQ_F16, LQ_BF16 or LQ_F32);
+ * fp32 arithmetic; Y may not alias H or R. */
 int locomp_amd_rms_norm(void* H, const void* R, const void* gamma, void* Y, int64_t M, int64_t K,
                         float eps, int dtype, void* stream);
+
+/* One decode-step link in one launch: the dequant-matmul of
+ * locomp_amd_dequant_matvec_int4 (N = weight rows) with
+ *   norm_weight != NULL: X is the hidden state and the matmul takes
+ *       rmsnorm(X[m]) = X[m] * rsqrt(sum(X[m]^2) / K + norm_eps) * norm_weight
+ *       (norm_weight [K] of X's dtype; each normalized activation rounded
+ *       to X's dtype, as locomp_amd_rms_norm would store it);
+ *   residual != NULL: O = X W^T + residual (residual [M, N] of O's dtype;
+ *       it may be O itself, the residual stream updated in place);
+ *   silu_mul != 0: gate|up rows interleaved as for
+ *       locomp_amd_dequant_matvec_int4_silu_mul, O [M, N / 2] (not with a
+ *       residual).
+ * Replaces, in examples/54_smollm2_inference.py's decode step (:494-554),
+ * rms_norm_kernel (:40-73) before a matvec and add_inplace_kernel
+ * (:164-167) after one: the layer's chain becomes norm+q|k|v, o+residual,
+ * norm+gate|up(SiLU * mul), down+residual.  No counterpart in the
+ * reference: it launches those kernels separately.  One launch on the row
+ * kernel for M = 1, K <= 4096, G % 32 == 0, 16-byte aligned X, W and
+ * norm_weight; otherwise staged through per-(device, stream) workspaces
+ * (the normalized activations, M x K; the fp32 product before a residual
+ * add, M x N x 4 bytes), held until the process ends; a capture on a stream
+ * without them returns LQ_ERR_SCRATCH. */
+int locomp_amd_dequant_matvec_int4_fused(const void* X, const void* W, const void* scales, void* O,
+                                         int64_t K_dim, int64_t HALF_K, int64_t NUM_SCALES,
+                                         int64_t GROUP_SIZE, int64_t N, int64_t M, int x_dtype,
+                                         int scale_dtype, int out_dtype, const void* norm_weight,
+                                         float norm_eps, const void* residual, int silu_mul,
+                                         void* stream);
 
 #ifdef __cplusplus
 }

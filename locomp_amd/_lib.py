@@ -51,6 +51,9 @@ SIGNATURES = {
     "locomp_amd_quantize_int8": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp],
     "locomp_amd_stream_read": [_vp, _i64, _vp, _vp],
     "locomp_amd_rms_norm": [_vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _int, _vp],
+    "locomp_amd_dequant_matvec_int4_fused": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                             _i64, _int, _int, _int, _vp, ctypes.c_float, _vp,
+                                             _int, _vp],
 }
 
 _lib = None

@@ -49,6 +49,9 @@ int launch_rows_silu_x(const void*, const void*, const void*, void*, int64_t, in
                        int64_t, int, int, int, hipStream_t);
 int launch_rms_norm(void*, const void*, const void*, void*, int64_t, int64_t, float, int,
                     hipStream_t);
+int launch_matvec_fused(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
+                        int64_t, int, int, int, const void*, float, const void*, bool, hipStream_t);
+int launch_add_rows(const float*, const void*, void*, int64_t, int, hipStream_t);
 int launch_quantize(int, const void*, void*, float*, int64_t, int64_t, int64_t, int, bool,
                     hipStream_t);
 int launch_silu_fast(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
@@ -222,7 +225,9 @@ const char* locomp_amd_strerror(int code) {
     case LQ_ERR_DTYPE: return "unknown dtype code";
     case LQ_ERR_NULL: return "null pointer for a non-empty problem";
     case LQ_ERR_POLICY: return "unknown kernel policy";
-    case LQ_ERR_SCRATCH: return "problem needs more scratch than the fixed buffer holds";
+    case LQ_ERR_SCRATCH:
+      return "problem needs scratch memory that is not available (the fixed buffer is too small, "
+             "or a workspace cannot be allocated during stream capture)";
     case LQ_ERR_NAME: return "unknown kernel name";
     default: break;
   }
@@ -452,11 +457,68 @@ int locomp_amd_quantize_int8(const void* W, void* Q, float* SCALES, int64_t N, i
 
 int locomp_amd_rms_norm(void* H, const void* R, const void* gamma, void* Y, int64_t M, int64_t K,
                         float eps, int dtype, void* stream) {
-  if (dtype != LQ_F16 && dtype != LQ_F32) return LQ_ERR_DTYPE;
+  if (!dtype_ok(dtype)) return LQ_ERR_DTYPE;
   if (M < 0 || K < 0 || M > kMax32 || K > kMax32) return LQ_ERR_SHAPE;
   if (M == 0 || K == 0) return LQ_OK;
   if (!H || !gamma || !Y) return LQ_ERR_NULL;
   return launch_rms_norm(H, R, gamma, Y, M, K, eps, dtype, static_cast<hipStream_t>(stream));
+}
+
+int locomp_amd_dequant_matvec_int4_fused(const void* X, const void* W, const void* scales, void* O,
+                                         int64_t K_dim, int64_t HALF_K, int64_t NUM_SCALES,
+                                         int64_t GROUP_SIZE, int64_t N, int64_t M, int x_dtype,
+                                         int scale_dtype, int out_dtype, const void* norm_weight,
+                                         float norm_eps, const void* residual, int silu_mul,
+                                         void* stream) {
+  int rc = check_common(K_dim, NUM_SCALES, GROUP_SIZE, N);
+  if (rc) return rc;
+  if (HALF_K * 2 != K_dim) return LQ_ERR_SHAPE;
+  if (!dtype_ok(x_dtype) || !dtype_ok(scale_dtype) || !dtype_ok(out_dtype)) return LQ_ERR_DTYPE;
+  if (M < 0 || (silu_mul && (residual || N % 2 != 0))) return LQ_ERR_SHAPE;
+  const int64_t on = silu_mul ? N / 2 : N;   // output columns
+  if (M == 0 || on == 0) return LQ_OK;
+  if (!O) return LQ_ERR_NULL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!norm_weight && !residual) {
+    if (silu_mul)
+      return locomp_amd_dequant_matvec_int4_silu_mul(X, W, scales, O, K_dim, HALF_K, NUM_SCALES,
+                                                     GROUP_SIZE, N / 2, M, x_dtype, scale_dtype,
+                                                     out_dtype, stream);
+    return matmul_dispatch<4>(X, W, scales, O, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
+                              out_dtype, st);
+  }
+  if (K_dim > 0 && (!X || !W || !scales)) return LQ_ERR_NULL;
+  if (fast_allowed() && K_dim > 0 && aligned(X, 16) && aligned(W, 16) && aligned(scales, 4) &&
+      (!norm_weight || aligned(norm_weight, 16))) {
+    rc = launch_matvec_fused(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
+                             out_dtype, norm_weight, norm_eps, residual, silu_mul != 0, st);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
+  // Staged: the normalized activations in workspace slot 4, the product in
+  // fp32 in slot 3 when a residual follows, then the residual add.
+  const void* Xn = X;
+  if (norm_weight && K_dim > 0) {
+    const size_t xs = x_dtype == LQ_F32 ? 4 : 2;
+    void* Y = stream_workspace(4, size_t(M) * size_t(K_dim) * xs, st);
+    if (Y == nullptr) return LQ_ERR_SCRATCH;
+    rc = launch_rms_norm(const_cast<void*>(X), nullptr, norm_weight, Y, M, K_dim, norm_eps,
+                         x_dtype, st);
+    if (rc != LQ_OK) return rc;
+    Xn = Y;
+  }
+  if (silu_mul)
+    return locomp_amd_dequant_matvec_int4_silu_mul(Xn, W, scales, O, K_dim, HALF_K, NUM_SCALES,
+                                                   GROUP_SIZE, N / 2, M, x_dtype, scale_dtype,
+                                                   out_dtype, stream);
+  if (!residual)
+    return matmul_dispatch<4>(Xn, W, scales, O, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype,
+                              out_dtype, st);
+  void* P = stream_workspace(3, size_t(M) * size_t(N) * sizeof(float), st);
+  if (P == nullptr) return LQ_ERR_SCRATCH;
+  rc = matmul_dispatch<4>(Xn, W, scales, P, K_dim, GROUP_SIZE, N, M, x_dtype, scale_dtype, LQ_F32,
+                          st);
+  if (rc != LQ_OK) return rc;
+  return launch_add_rows(static_cast<const float*>(P), residual, O, M * N, out_dtype, st);
 }
 
 }  // extern "C"

@@ -26,11 +26,44 @@ namespace lq {
 // 136 x the activation sum; fp32 takes the nibbles as floats q (byte
 // conversions) in fp32 FMAs with the activations as loaded, the bias 8 x
 // their sum.  SD / OD = kRT take the scale / output dtypes from sd_rt / od_rt.
-template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3, int XD = LQ_F16>
+// FUSE (decode-step fusions, examples/54_smollm2_inference.py:40-73,
+// 164-167): kFuseNorm = X is the hidden state, used as
+// rmsnorm(X[m]) * gamma (gamma of X's dtype; every wave forms the row's sum
+// of squares from the activations it loads anyway, then rounds each
+// normalized activation to X's dtype as a separate norm launch would store
+// it); kFuseRes = O = X W^T + R (R of O's dtype, read before the store, so
+// R may be O itself: the residual stream updated in place).
+constexpr int kFuseNorm = 1, kFuseRes = 2;
+
+// Element i of an fp32 / fp16 / bf16 array whose dtype `dt` is known only at
+// run time, without a branch: two 16-bit loads (the bits, for fp32 both
+// halves), converted where the value is used.  (A uniform branch around the
+// load makes the compiler wait for every load in flight where the paths
+// join, and a conversion next to the load waits for it: either serialized
+// the weight loads behind it.)
+struct Bits16x2 {
+  uint32_t lo, hi;   // each a zero-extended 16-bit load
+};
+__device__ __forceinline__ Bits16x2 load_bits_sel(const void* a, size_t i, int dt) {
+  const bool f32 = dt == LQ_F32;
+  const uint16_t* p = static_cast<const uint16_t*>(a) + (f32 ? 2 * i : i);
+  return Bits16x2{p[0], p[f32 ? 1 : 0]};
+}
+__device__ __forceinline__ float bits_to_f32_sel(Bits16x2 b, int dt) {
+  const float ff = __uint_as_float(b.lo | (b.hi << 16));
+  const float fh = float(__builtin_bit_cast(half_t, uint16_t(b.lo)));
+  const float fb = __uint_as_float(b.lo << 16);
+  return dt == LQ_F32 ? ff : dt == LQ_F16 ? fh : fb;
+}
+
+template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3, int XD = LQ_F16,
+          int FUSE = 0>
 __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
     const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
-    int od_rt = 0) {
+    int od_rt = 0, const void* __restrict__ gamma = nullptr, float eps = 0.f,
+    const void* R = nullptr) {
+  static_assert(!(EPI && (FUSE & kFuseRes)), "the residual add takes the plain store");
   typedef typename Elem<SD == kRT ? LQ_F32 : SD>::T stype;   // (kRT: converted at load)
   constexpr bool kH = XD == LQ_F16;
   constexpr bool kF = XD == LQ_F32;
@@ -67,9 +100,39 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
         }
       }
     }
+  // (kFuseNorm) the norm weights for the same k-ranges, loaded with the
+  // activations; (kFuseRes) the residual of the row this lane stores
+  u32x4_t gv[NSEG][NP][4];
+  if constexpr ((FUSE & kFuseNorm) != 0) {
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c) {
+      const int k0 = min(c * 2048 + lane * 32, K - 32);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (kF) {
+          const float* gf = static_cast<const float*>(gamma) + k0 + e * 8;
+          gv[c][0][e] = *reinterpret_cast<const u32x4_t*>(gf);
+          gv[c][1][e] = *reinterpret_cast<const u32x4_t*>(gf + 4);
+        } else {
+          gv[c][0][e] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(gamma) + k0 + e * 8);
+        }
+      }
+    }
+  }
+  Bits16x2 rres[M_];
+  if constexpr ((FUSE & kFuseRes) != 0) {
+    int row = 0, w2 = 32;   // the row this lane stores (as the final reduction leaves it)
+#pragma unroll
+    for (int c2 = RW; c2 > 1; c2 >>= 1, w2 >>= 1) row = row * 2 + ((lane & w2) ? 1 : 0);
+#pragma unroll
+    for (int m = 0; m < M_; ++m)
+      rres[m] = load_bits_sel(R, size_t(m < M ? m : 0) * N + min(n0 + row, N - 1),
+                              OD == kRT ? od_rt : OD);
+  }
   // 2. scales of (row, segment)
   const stype* sp = static_cast<const stype*>(S);
   stype sv[RW][NSEG];
+  Bits16x2 svb[RW][NSEG];   // (kRT: the bits, converted at use)
 #pragma unroll
   for (int r = 0; r < RW; ++r)
 #pragma unroll
@@ -78,7 +141,7 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
       const int n = min(n0 + r, N - 1);
       const size_t si = size_t(n) * num_scales + k0 / group;
       if constexpr (SD == kRT)
-        sv[r][c] = load_scale<kRT>(static_cast<const uint8_t*>(S) + si * (sd_rt == LQ_F32 ? 4 : 2), sd_rt);
+        svb[r][c] = load_bits_sel(S, si, sd_rt);
       else
         sv[r][c] = sp[si];
     }
@@ -96,6 +159,90 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
     }
   __builtin_amdgcn_sched_barrier(0);
 
+  if constexpr ((FUSE & kFuseNorm) != 0) {
+    // rmsnorm of each activation row over all K (a wave's lanes hold every
+    // k once: lane k-ranges past K, clamped to the row's end, are left out);
+    // after every load has been issued, so only the activations' and norm
+    // weights' latency is waited for here
+    auto rnd = [](float f) -> uint32_t {   // to X's dtype, as bits
+      if constexpr (kF) return __float_as_uint(f);
+      else if constexpr (kH) return __builtin_bit_cast(uint16_t, half_t(f));
+      else return uint32_t(f32_to_bf16(f));
+    };
+    // The 4 waves hold the same activations: wave w normalizes slice e = w
+    // (8 of each lane's 32 k) and the slices are exchanged through LDS, a
+    // quarter of the VALU work per wave (every wave doing all 32 cost the
+    // 49152 x 576 LM head 5 us).
+    __shared__ float nss[M_][4];
+    __shared__ u32x4_t nx[M_][NSEG][4][NP][64];
+    // element j (0..7) of slice e of a loaded group as fp32
+    auto elem8 = [](const u32x4_t (&v)[NP][4], int e, int j) {
+      if constexpr (kF) {
+        const u32x4_t q = v[j >> 2][e];
+        const int t = j & 3;
+        return __uint_as_float(t == 0 ? q.x : t == 1 ? q.y : t == 2 ? q.z : q.w);
+      } else {
+        const u32x4_t q = v[0][e];
+        const int t = j >> 1;
+        const uint32_t d = t == 0 ? q.x : t == 1 ? q.y : t == 2 ? q.z : q.w;
+        const uint16_t bb = uint16_t((j & 1) ? d >> 16 : d);
+        if constexpr (kH) return float(__builtin_bit_cast(half_t, bb));
+        else return __uint_as_float(uint32_t(bb) << 16);
+      }
+    };
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (e != wave) continue;   // (uniform: one slice per wave)
+#pragma unroll
+      for (int m = 0; m < M_; ++m) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < NSEG; ++c) {
+          float sc = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float v = elem8(xv[m][c], e, j);
+            sc = fmaf(v, v, sc);
+          }
+          ss += c * 2048 + lane * 32 < K ? sc : 0.f;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) nss[m][e] = ss;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (e != wave) continue;
+#pragma unroll
+      for (int m = 0; m < M_; ++m) {
+        const float rms = rsqrtf((nss[m][0] + nss[m][1] + nss[m][2] + nss[m][3]) / float(K) + eps);
+#pragma unroll
+        for (int c = 0; c < NSEG; ++c) {
+          uint32_t y[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) y[j] = rnd(elem8(xv[m][c], e, j) * rms * elem8(gv[c], e, j));
+          if constexpr (kF) {
+            nx[m][c][e][0][lane] = u32x4_t{y[0], y[1], y[2], y[3]};
+            nx[m][c][e][1][lane] = u32x4_t{y[4], y[5], y[6], y[7]};
+          } else {
+            nx[m][c][e][0][lane] = u32x4_t{y[0] | (y[1] << 16), y[2] | (y[3] << 16), y[4] | (y[5] << 16),
+                                           y[6] | (y[7] << 16)};
+          }
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M_; ++m)
+#pragma unroll
+      for (int c = 0; c < NSEG; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int h = 0; h < NP; ++h) xv[m][c][h][e] = nx[m][c][e][h][lane];
+  }
   // 4. permute activations, bias correction per (m, segment)
   const uint32_t ones = kH ? 0x3C003C00u : 0x3F803F80u;   // (1, 1) as fp16 / bf16
   float corr[M_][NSEG];
@@ -175,7 +322,8 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
 #pragma unroll
       for (int m = 0; m < M_; ++m) part[m] = (pe[m][0] + pe[m][1]) + (pe[m][2] + pe[m][3]);
       float sc;
-      if constexpr (SD == LQ_F32 || SD == kRT) sc = sv[r][c];
+      if constexpr (SD == kRT) sc = bits_to_f32_sel(svb[r][c], sd_rt);
+      else if constexpr (SD == LQ_F32) sc = sv[r][c];
       else if constexpr (SD == LQ_F16) sc = float(sv[r][c]);
       else sc = bf16_to_f32(sv[r][c]);
       sc = valid ? sc : 0.f;
@@ -232,8 +380,12 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
         store_out<OD>(O, size_t(m) * (N >> 1) + ((n0 + row) >> 1), g / (1.0f + expf(-g)) * other, od_rt);
       }
     } else {
-      if ((lane & lowmask) == lowmask && m < M && n0 + row < N)
-        store_out<OD>(O, size_t(m) * N + n0 + row, v[0], od_rt);
+      if ((lane & lowmask) == lowmask && m < M && n0 + row < N) {
+        const size_t at = size_t(m) * N + n0 + row;
+        float y = v[0];
+        if constexpr ((FUSE & kFuseRes) != 0) y += bits_to_f32_sel(rres[m], OD == kRT ? od_rt : OD);
+        store_out<OD>(O, at, y, od_rt);
+      }
     }
   }
 }
