@@ -432,6 +432,11 @@ def main():
             if want(f"gemv_{xd}"):
                 run_case(f"gemv_w4a{xd}_M{M}", Case("matvec", 4, M, c3["N"], c3["K"], c3["G"],
                                                               c3["lo"], c3["hi"], xd=xd), "hbm")
+    if want("gemv_g16"):
+        # scale groups of 16 (G % 32 != 0): the fp32-FMA / dot2 VALU kernel
+        for xd, M in (("f16", 1), ("f16", 16), ("f32", 16)):
+            run_case(f"gemv_w4a{'16' if xd == 'f16' else xd}_g16_M{M}",
+                     Case("matvec", 4, M, c3["N"], c3["K"], 16, c3["lo"], c3["hi"], xd=xd), "hbm")
     if want("gemm_prefill_bf16"):
         c = synth.CFG5A
         run_case("gemm_prefill_w4abf16_2048x4096x4096_g128",
@@ -444,8 +449,9 @@ def main():
         run_case("w8a32_M4_512x512_cfg1",
                  Case("matvec", 8, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"], xd="f32"), "hbm")
     if want("gemm_prefill_f32"):
-        # fp32 activations (the reference's dtype): exact bf16 parts as 3 M
-        # rows on the bf16 GEMM, then the part rows added
+        # fp32 activations (the reference's dtype): two round-to-nearest
+        # bf16 parts per row as 2 M rows on the bf16 GEMM, each row's pair
+        # of part products added in its epilogue
         c = synth.CFG5A
         run_case("gemm_prefill_w4af32_2048x4096x4096_g128",
                  Case("matvec", 4, c["M"], c["N"], c["K"], c["G"], c["lo"], c["hi"],
