@@ -29,6 +29,23 @@ int launch_split_reduce(const float* P, void* O, int64_t M, int64_t N, int split
 
 constexpr int kGWaves = 4;
 
+// A run-time-dtype (fp32 / fp16 / bf16) element as its bits, loaded as two
+// 16-bit halves without a branch, converted where used.
+struct Bits16 {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ Bits16 load_bits16(const void* a, size_t i, int dt) {
+  const bool f32 = dt == LQ_F32;
+  const uint16_t* p = static_cast<const uint16_t*>(a) + (f32 ? 2 * i : i);
+  return Bits16{p[0], p[f32 ? 1 : 0]};
+}
+__device__ __forceinline__ float bits16_to_f32(Bits16 b, int dt) {
+  const float ff = __uint_as_float(b.lo | (b.hi << 16));
+  const float fh = float(__builtin_bit_cast(half_t, uint16_t(b.lo)));
+  const float fb = __uint_as_float(b.lo << 16);
+  return dt == LQ_F32 ? ff : dt == LQ_F16 ? fh : fb;
+}
+
 // One dword of weights -> WPD exact floats (int4: q - 8, low nibble first;
 // int8: q).
 template <int WBITS>
@@ -222,6 +239,131 @@ __global__ __launch_bounds__(64 * kGWaves) void group_valu_kernel(
   }
 }
 
+// Decode rows (M <= 4): lane l of a wave walks dword l of every 64-dword
+// segment of each of the wave's RW weight rows (one coalesced 256-byte load
+// per row and segment), so a lane's 8 (int4) / 4 (int8) weights lie in one
+// scale group (G % 8 / % 4) and its partial sum is scaled at once; the next
+// SB segments' weights, scales and activations load while these compute;
+// the lanes are summed at the end (a butterfly per output).
+template <int WBITS, int XD, int M_, int RW, int SB, bool EPI>
+__global__ __launch_bounds__(256) void group_rows_kernel(
+    const void* __restrict__ X, const uint32_t* __restrict__ W, const void* __restrict__ S,
+    void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd, int od) {
+  constexpr int kWpd = WBITS == 4 ? 8 : 4;
+  constexpr int kXW = XD == LQ_F32 ? kWpd : kWpd / 2;   // activation dwords per lane and row
+  static_assert(!EPI || RW % 2 == 0, "gate / up pairs within one wave");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = (blockIdx.x * 4 + wave) * RW;
+  const int row_dw = K / kWpd;
+  const int nseg = (row_dw + 63) / 64;
+  const int xb = XD == LQ_F32 ? 4 : 2;
+
+  // SB segments per step (RW x SB weight loads in flight per wave)
+  struct Seg {
+    uint32_t w[SB][RW];
+    Bits16 s[SB][RW];
+    uint32_t x[SB][M_][kXW];
+  };
+  auto fetch = [&](Seg& g, int c0) {
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      // (lanes past the row: its last dword, not used)
+      const int d = min((c0 + j) * 64 + lane, row_dw - 1);
+      const int gi = int(uint32_t(d) * kWpd / uint32_t(group));
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        const int n = min(n0 + r, N - 1);
+        g.w[j][r] = W[size_t(n) * row_dw + d];
+        g.s[j][r] = load_bits16(S, size_t(n) * num_scales + gi, sd);
+      }
+#pragma unroll
+      for (int m = 0; m < M_; ++m) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(
+            static_cast<const uint8_t*>(X) + (size_t(m < M ? m : 0) * K + size_t(d) * kWpd) * xb);
+#pragma unroll
+        for (int e = 0; e < kXW; ++e) g.x[j][m][e] = p[e];
+      }
+    }
+  };
+  float acc[M_][RW];
+#pragma unroll
+  for (int m = 0; m < M_; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) acc[m][r] = 0.f;
+  Seg cur, nxt;
+  fetch(cur, 0);
+  for (int c = 0; c < nseg; c += SB) {
+    if (c + SB < nseg) fetch(nxt, c + SB);
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const bool valid = (c + j) * 64 + lane < row_dw;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        float w[8];
+        decode_dword<WBITS>(cur.w[j][r], w);
+        uint32_t wp[4];
+        if constexpr (XD != LQ_F32) {
+#pragma unroll
+          for (int e = 0; e < kWpd / 2; ++e) wp[e] = pack_pair<XD>(w[2 * e], w[2 * e + 1]);
+        }
+        const float sc = valid ? bits16_to_f32(cur.s[j][r], sd) : 0.f;
+#pragma unroll
+        for (int m = 0; m < M_; ++m) {
+          float a = 0.f;
+#pragma unroll
+          for (int e = 0; e < kXW; ++e) {
+            if constexpr (XD == LQ_F32) a = fmaf(__uint_as_float(cur.x[j][m][e]), w[e], a);
+            else a = dot2<XD>(cur.x[j][m][e], wp[e], a);
+          }
+          acc[m][r] = fmaf(a, sc, acc[m][r]);
+        }
+      }
+    }
+    cur = nxt;
+  }
+#pragma unroll
+  for (int m = 0; m < M_; ++m) {
+    float v[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      v[r] = acc[m][r];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v[r] += __shfl_xor(v[r], off, 64);
+    }
+    if (lane != 0 || m >= M) continue;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int n = n0 + r;
+      if constexpr (EPI) {
+        if ((r & 1) == 0 && n + 1 < N)
+          store_out<kRT>(O, size_t(m) * (N / 2) + n / 2, v[r] / (1.0f + expf(-v[r])) * v[r + 1], od);
+      } else {
+        if (n < N) store_out<kRT>(O, size_t(m) * N + n, v[r], od);
+      }
+    }
+  }
+}
+
+template <int WBITS, int XD, int M_, bool EPI>
+static void launch_group_rows_t(const void* X, const void* W, const void* S, void* O, int64_t M,
+                                int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  constexpr int kRW = 4;
+  constexpr int kSB = 4 / M_;   // (the activations of M_ rows x SB segments in registers)
+  hipLaunchKernelGGL((group_rows_kernel<WBITS, XD, M_, kRW, kSB, EPI>),
+                     dim3(unsigned((N + 4 * kRW - 1) / (4 * kRW))), dim3(256), 0, st, X,
+                     static_cast<const uint32_t*>(W), S, O, int(M), int(N), int(K), int(K / G),
+                     int(G), sd, od);
+}
+
+template <int WBITS, int XD, bool EPI>
+static void launch_group_rows(const void* X, const void* W, const void* S, void* O, int64_t M,
+                              int64_t N, int64_t K, int64_t G, int sd, int od, hipStream_t st) {
+  if (M <= 1) launch_group_rows_t<WBITS, XD, 1, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+  else if (M <= 2) launch_group_rows_t<WBITS, XD, 2, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+  else launch_group_rows_t<WBITS, XD, 4, EPI>(X, W, S, O, M, N, K, G, sd, od, st);
+}
+
 template <int WBITS, int XD, bool EPI, bool VEC>
 static void launch_group_mt(const void* X, const void* W, const void* S, void* O, float* P,
                             int64_t M, int64_t N, int64_t K, int64_t G, int unit, int splits,
@@ -255,6 +397,14 @@ int launch_group_valu(const void* X, const void* W, const void* S, void* O, int6
     return LQ_ERR_SHAPE;
   // k split over workgroups until about two workgroups per CU, each wave
   // keeping at least 4 groups
+  if (M <= 4) {   // decode rows: lanes along k
+#define LQ_GR(XD_) launch_group_rows<WBITS, XD_, EPI>(X, W, S, O, M, N, K, G, sd, od, st)
+    if (xd == LQ_F32) LQ_GR(LQ_F32);
+    else if (xd == LQ_F16) LQ_GR(LQ_F16);
+    else LQ_GR(LQ_BF16);
+#undef LQ_GR
+    return check_launch();
+  }
   // run units: whole groups, and whole 8-dword blocks when the rows allow
   // 16-byte loads
   const int64_t row_dw = K / kWpd, gdw = G / kWpd;
