@@ -100,6 +100,32 @@ def test_silu_mul_abi_validates_without_a_gpu():
     assert f(NULL, NULL, NULL, NULL, 64, 32, 2, 32, 0, 1, 1, 1, 1, NULL) == 0    # I = 0: nothing to do
 
 
+def test_fused_abi_validates_without_a_gpu():
+    lib = _lib.load()
+    f = lib.locomp_amd_dequant_matvec_int4_fused
+    # (X, W, scales, O, K_dim, HALF_K, NUM_SCALES, GROUP_SIZE, N, M, xd, sd, od,
+    #  norm_weight, eps, residual, silu_mul, stream)
+    ok = (64, 32, 2, 32, 8, 1, 1, 1, 1)
+    assert f(P, P, P, P, 64, 31, 2, 32, 8, 1, 1, 1, 1, P, 1e-5, None, 0, NULL) == _lib.ERR_SHAPE  # HALF_K
+    assert f(P, P, P, P, 64, 32, 3, 32, 8, 1, 1, 1, 1, P, 1e-5, None, 0, NULL) == _lib.ERR_SHAPE  # G
+    assert f(P, P, P, P, *ok, P, 1e-5, P, 1, NULL) == _lib.ERR_SHAPE        # SiLU * mul with a residual
+    assert f(P, P, P, P, 64, 32, 2, 32, 7, 1, 1, 1, 1, P, 1e-5, None, 1, NULL) == _lib.ERR_SHAPE  # odd rows
+    assert f(P, P, P, P, 64, 32, 2, 32, 8, 1, 7, 1, 1, P, 1e-5, None, 0, NULL) == _lib.ERR_DTYPE
+    assert f(NULL, P, P, P, *ok, P, 1e-5, None, 0, NULL) == _lib.ERR_NULL
+    assert f(P, P, P, NULL, *ok, P, 1e-5, P, 0, NULL) == _lib.ERR_NULL
+    assert f(NULL, NULL, NULL, NULL, 64, 32, 2, 32, 8, 0, 1, 1, 1, P, 1e-5, P, 0, NULL) == 0  # M = 0
+
+
+def test_rms_norm_abi_validates_without_a_gpu():
+    lib = _lib.load()
+    f = lib.locomp_amd_rms_norm
+    # (H, R, gamma, Y, M, K, eps, dtype, stream); fp16, bf16 and fp32 accepted
+    assert f(P, NULL, P, P, 1, 576, 1e-5, 7, NULL) == _lib.ERR_DTYPE
+    assert f(P, NULL, P, P, -1, 576, 1e-5, 2, NULL) == _lib.ERR_SHAPE
+    assert f(NULL, NULL, P, P, 1, 576, 1e-5, 2, NULL) == _lib.ERR_NULL
+    assert f(NULL, NULL, NULL, NULL, 0, 576, 1e-5, 2, NULL) == 0
+
+
 def test_interleave_gate_up():
     import locomp_amd as lq
     g = np.arange(12, dtype=np.uint8).reshape(3, 4)
