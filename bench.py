@@ -433,7 +433,8 @@ def main():
                 run_case(f"gemv_w4a{xd}_M{M}", Case("matvec", 4, M, c3["N"], c3["K"], c3["G"],
                                                               c3["lo"], c3["hi"], xd=xd), "hbm")
     if want("gemv_g16"):
-        # scale groups of 16 (G % 32 != 0): the fp32-FMA / dot2 VALU kernel
+        # scale groups of 16 (G % 32 != 0): the row kernel with a scale per 16 k
+        # at M = 1, the fp32-FMA / dot2 VALU kernel at M = 16
         for xd, M in (("f16", 1), ("f16", 16), ("f32", 16)):
             run_case(f"gemv_w4a{'16' if xd == 'f16' else xd}_g16_M{M}",
                      Case("matvec", 4, M, c3["N"], c3["K"], 16, c3["lo"], c3["hi"], xd=xd), "hbm")

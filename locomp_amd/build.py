@@ -16,7 +16,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJDIR = PKG / "_build"
 LIB = PKG / "_liblocomp_amd.so"
-SOURCES = ["dequant.hip", "gemv_w4.hip", "gemv_w8.hip", "gemv_x4.hip", "gemv_x8.hip", "gemv_xsilu.hip", "gemv_generic.hip", "gemv_group.hip", "gemv_fused.hip", "gemm.hip", "quantize.hip",
+SOURCES = ["dequant.hip", "gemv_w4.hip", "gemv_w8.hip", "gemv_x4.hip", "gemv_x8.hip", "gemv_xsilu.hip", "gemv_generic.hip", "gemv_group.hip", "gemv_rows16.hip", "gemv_fused.hip", "gemm.hip", "quantize.hip",
            "stream.hip", "norm.hip", "capi.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

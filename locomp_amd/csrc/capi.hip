@@ -23,6 +23,9 @@ int launch_gemm_pairs(const void*, const void*, const void*, void*, int64_t, int
 template <int WBITS, bool EPI>
 int launch_group_valu(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                       int64_t, int, int, int, hipStream_t, const FixedScratch*);
+template <bool EPI>
+int launch_rows_g16(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, int64_t,
+                    int, int, int, hipStream_t);
 template <int WBITS, int XD, bool EPI>
 int launch_tile_rows_x(const void*, const void*, const void*, void*, int64_t, int64_t, int64_t,
                        int64_t, int, int, hipStream_t);
@@ -205,6 +208,12 @@ static int matmul_dispatch(const void* X, const void* W, const void* S, void* O,
       if (rc != LQ_ERR_SHAPE) return rc;
     }
   }
+  if (fast_common && WBITS == 4 && M <= 2 && G % 32 != 0 && G % 16 == 0) {
+    // scale groups of 16-k multiples at M <= 2: the row kernel with a scale
+    // per 16 k
+    const int rc = launch_rows_g16<false>(X, W, S, O, M, N, K, G, xd, sd, od, st);
+    if (rc != LQ_ERR_SHAPE) return rc;
+  }
   if (fast_allowed() && small_enough) {
     // scale groups the MFMA kernels do not take (G % 32 != 0), unaligned
     // operands, and what else is left: fp32 FMAs on the VALU kernel
@@ -350,6 +359,12 @@ int locomp_amd_dequant_matvec_int4_silu_mul(const void* X, const void* W, const 
     else if (fused)
       rc = launch_silu_fast(X, W, scales, O, M, N, K_dim, GROUP_SIZE, scale_dtype, out_dtype, st);
     if (rc != LQ_ERR_SHAPE) return rc;
+    if (GROUP_SIZE % 32 != 0 && GROUP_SIZE % 16 == 0 && M <= 2 && K_dim % 8 == 0) {
+      // scale groups of 16-k multiples: the row kernel with a scale per 16 k
+      rc = launch_rows_g16<true>(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,
+                                 out_dtype, st);
+      if (rc != LQ_ERR_SHAPE) return rc;
+    }
     if (!fused && K_dim % 8 == 0) {
       // bf16 / fp32 activations or bf16 dtypes, M <= 2: the row kernel
       rc = launch_rows_silu_x(X, W, scales, O, M, N, K_dim, GROUP_SIZE, x_dtype, scale_dtype,

@@ -1,4 +1,4 @@
-// gemv_rows_kernel: row-contiguous int4 decode GEMV (M <= 2, G % 32), with the SiLU * mul epilogue.
+// gemv_rows_kernel: row-contiguous int4 decode GEMV (M <= 2, G % 32 or G % 16), with the SiLU * mul epilogue.
 // Part of the decode GEMV kernels; see gemv_impl.h for the kernel choice.
 #pragma once
 #include "gemv_common.h"
@@ -33,6 +33,9 @@ namespace lq {
 // normalized activation to X's dtype as a separate norm launch would store
 // it); kFuseRes = O = X W^T + R (R of O's dtype, read before the store, so
 // R may be O itself: the residual stream updated in place).
+// G16: scale groups of 16 k multiples (G % 16 == 0, e.g. G = 16 or 48): each
+// half of a lane's 32 k (16-aligned, so inside one group) has its own scale
+// and bias correction.
 constexpr int kFuseNorm = 1, kFuseRes = 2;
 
 // Element i of an fp32 / fp16 / bf16 array whose dtype `dt` is known only at
@@ -57,7 +60,7 @@ __device__ __forceinline__ float bits_to_f32_sel(Bits16x2 b, int dt) {
 }
 
 template <int M_, int NSEG, int RW, int SD, int OD, bool EPI = false, int OCC = 3, int XD = LQ_F16,
-          int FUSE = 0>
+          int FUSE = 0, bool G16 = false>
 __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
     const void* __restrict__ X, const uint8_t* __restrict__ W, const void* __restrict__ S,
     void* __restrict__ O, int M, int N, int K, int num_scales, int group, int sd_rt = 0,
@@ -68,6 +71,7 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
   constexpr bool kH = XD == LQ_F16;
   constexpr bool kF = XD == LQ_F32;
   constexpr int NP = kF ? 2 : 1;                // u32x4 per 8 activations
+  constexpr int NH = G16 ? 2 : 1;               // scales per lane k-range
   typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
   auto dot2 = [](uint32_t a, uint32_t b, float c) {
     if constexpr (kH) return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
@@ -129,22 +133,24 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
       rres[m] = load_bits_sel(R, size_t(m < M ? m : 0) * N + min(n0 + row, N - 1),
                               OD == kRT ? od_rt : OD);
   }
-  // 2. scales of (row, segment)
+  // 2. scales of (row, segment[, half])
   const stype* sp = static_cast<const stype*>(S);
-  stype sv[RW][NSEG];
-  Bits16x2 svb[RW][NSEG];   // (kRT: the bits, converted at use)
+  stype sv[RW][NSEG][NH];
+  Bits16x2 svb[RW][NSEG][NH];   // (kRT: the bits, converted at use)
 #pragma unroll
   for (int r = 0; r < RW; ++r)
 #pragma unroll
-    for (int c = 0; c < NSEG; ++c) {
-      const int k0 = min(c * 2048 + lane * 32, K - 32);
-      const int n = min(n0 + r, N - 1);
-      const size_t si = size_t(n) * num_scales + k0 / group;
-      if constexpr (SD == kRT)
-        svb[r][c] = load_bits_sel(S, si, sd_rt);
-      else
-        sv[r][c] = sp[si];
-    }
+    for (int c = 0; c < NSEG; ++c)
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        const int k0 = min(c * 2048 + lane * 32, K - 32) + 16 * h;
+        const int n = min(n0 + r, N - 1);
+        const size_t si = size_t(n) * num_scales + k0 / group;
+        if constexpr (SD == kRT)
+          svb[r][c][h] = load_bits_sel(S, si, sd_rt);
+        else
+          sv[r][c][h] = sp[si];
+      }
   __builtin_amdgcn_sched_barrier(0);
   // 3. all weights of this wave
   u32x4_t wv[RW][NSEG];
@@ -245,32 +251,39 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
   }
   // 4. permute activations, bias correction per (m, segment)
   const uint32_t ones = kH ? 0x3C003C00u : 0x3F803F80u;   // (1, 1) as fp16 / bf16
-  float corr[M_][NSEG];
+  // (G16: dwords e = 0, 1 are the first 16 k, e = 2, 3 the second)
+  float corr[M_][NSEG][NH];
 #pragma unroll
   for (int m = 0; m < M_; ++m)
 #pragma unroll
     for (int c = 0; c < NSEG; ++c) {
-      float sum = 0.f;
+      float sum[NH];
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh) sum[hh] = 0.f;
       if constexpr (kF) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const u32x4_t v = xv[m][c][h][e];
-            sum += (__uint_as_float(v.x) + __uint_as_float(v.y)) + (__uint_as_float(v.z) + __uint_as_float(v.w));
+            sum[G16 ? e >> 1 : 0] +=
+                (__uint_as_float(v.x) + __uint_as_float(v.y)) + (__uint_as_float(v.z) + __uint_as_float(v.w));
           }
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+          float& su = sum[G16 ? e >> 1 : 0];
           xv[m][c][0][e] = xperm8(xv[m][c][0][e]);
-          sum = dot2(xv[m][c][0][e].x, ones, sum);
-          sum = dot2(xv[m][c][0][e].y, ones, sum);
-          sum = dot2(xv[m][c][0][e].z, ones, sum);
-          sum = dot2(xv[m][c][0][e].w, ones, sum);
+          su = dot2(xv[m][c][0][e].x, ones, su);
+          su = dot2(xv[m][c][0][e].y, ones, su);
+          su = dot2(xv[m][c][0][e].z, ones, su);
+          su = dot2(xv[m][c][0][e].w, ones, su);
         }
       }
       const bool valid = (m < M) && (c * 2048 + lane * 32 < K);
-      corr[m][c] = valid ? sum * (kF ? 8.0f : kH ? kInt4Bias : 136.0f) : 0.f;
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh)
+        corr[m][c][hh] = valid ? sum[hh] * (kF ? 8.0f : kH ? kInt4Bias : 136.0f) : 0.f;
     }
   const uint32_t magic = opaque_u32(kH ? 0x64006400u : 0x43004300u);
 
@@ -318,17 +331,25 @@ __global__ __launch_bounds__(256, OCC) void gemv_rows_kernel(
           }
         }
       }
-      float part[M_];
+      float sc[NH];
 #pragma unroll
-      for (int m = 0; m < M_; ++m) part[m] = (pe[m][0] + pe[m][1]) + (pe[m][2] + pe[m][3]);
-      float sc;
-      if constexpr (SD == kRT) sc = bits_to_f32_sel(svb[r][c], sd_rt);
-      else if constexpr (SD == LQ_F32) sc = sv[r][c];
-      else if constexpr (SD == LQ_F16) sc = float(sv[r][c]);
-      else sc = bf16_to_f32(sv[r][c]);
-      sc = valid ? sc : 0.f;
+      for (int h = 0; h < NH; ++h) {
+        if constexpr (SD == kRT) sc[h] = bits_to_f32_sel(svb[r][c][h], sd_rt);
+        else if constexpr (SD == LQ_F32) sc[h] = sv[r][c][h];
+        else if constexpr (SD == LQ_F16) sc[h] = float(sv[r][c][h]);
+        else sc[h] = bf16_to_f32(sv[r][c][h]);
+        sc[h] = valid ? sc[h] : 0.f;
+      }
 #pragma unroll
-      for (int m = 0; m < M_; ++m) acc[m][r] += (part[m] - corr[m][c]) * sc;
+      for (int m = 0; m < M_; ++m) {
+        if constexpr (G16) {
+          acc[m][r] += ((pe[m][0] + pe[m][1]) - corr[m][c][0]) * sc[0];
+          acc[m][r] += ((pe[m][2] + pe[m][3]) - corr[m][c][1]) * sc[1];
+        } else {
+          const float part = (pe[m][0] + pe[m][1]) + (pe[m][2] + pe[m][3]);
+          acc[m][r] += (part - corr[m][c][0]) * sc[0];
+        }
+      }
       // consume in load order: no hoisting of later rows' decode (register
       // pressure) and no early waits on their loads
       __builtin_amdgcn_sched_barrier(0);

@@ -2,7 +2,9 @@
 the reference accepts any G dividing K, examples/38_quantized_matmul.py:
 141-155) and for activations too unaligned for them: the fp32-FMA VALU
 kernel (`gemv_group.hip`), every activation dtype, int4 and int8, with and
-without the k split over workgroups, and the gate|up SiLU * mul epilogue.
+without the k split over workgroups, and the gate|up SiLU * mul epilogue;
+at M <= 2 with G % 16 == 0 the row kernel with a scale per 16 k
+(`gemv_rows16.hip`).
 
 Oracle: the restated reference NumPy path on the values the kernel sees.
 Bars: fp32 activations and outputs rtol 1e-4 (+ atol 1e-5 max|Y|); fp16 /
@@ -82,8 +84,34 @@ def test_small_groups(wbits, M, N, K, G, xd, sd, od):
     _check(_out(Og, od, (M, N)), np.asarray(want, np.float64), xd, od)
 
 
+@pytest.mark.parametrize("M,N,K,G", [
+    (1, 11008, 4096, 16),       # 2 segments, 4 rows per wave
+    (2, 1000, 4096, 16),        # two activation rows
+    (1, 700, 10240, 16),        # 5 segments on the 6-segment kernel, one row per wave
+    (1, 513, 14400, 48),        # 8 segments, the last partial; groups of 3 halves
+    (2, 3000, 1440, 48),        # one partial segment, one row per wave
+    (1, 4100, 2080, 80),        # ragged last workgroup
+])
+@pytest.mark.parametrize("xd,sd,od", [("f16", "f16", "f16"), ("bf16", "bf16", "bf16"),
+                                      ("f32", "f32", "f32"), ("f16", "f32", "bf16")])
+def test_row_kernel_half_groups(M, N, K, G, xd, sd, od):
+    """int4, M <= 2, G a multiple of 16 but not of 32: the row kernel with a
+    scale per 16 k (fp32 activations: M = 1, K <= 4096; other shapes take
+    the VALU kernel), against the oracle."""
+    X, W, S = synth.matvec_case(4, M, N, K, G, 0.001, 0.01, x_dtype=np.float32,
+                                s_dtype=np.float32, seed=M + N + K + G)
+    Og = lq.empty((M, N), lq.bfloat16 if od == "bf16" else NP[od])
+    lq.dequant_matvec_int4[(N,), (128,)](_dev(X, xd), lq.tensor(W), _dev(S, sd), Og, K, K // 2, K // G, G)
+    want = ref.fast_numpy_matvec_int4(_used(X, xd), W, _used(S, sd), G)
+    _check(_out(Og, od, (M, N)), np.asarray(want, np.float64), xd, od)
+
+
 @pytest.mark.parametrize("M,I,K,G,xd", [
     (1, 1536, 576, 16, "f32"),
+    (2, 1000, 4096, 16, "f16"),     # row kernel with the epilogue
+    (1, 768, 12288, 48, "bf16"),    # 6 segments, 2 rows per wave
+    (1, 500, 14336, 16, "f16"),     # 7 segments: the VALU kernel
+    (2, 600, 2048, 16, "bf16"),
     (4, 700, 2048, 16, "bf16"),
     (24, 300, 1024, 8, "f16"),
     (130, 256, 480, 48, "f32"),
