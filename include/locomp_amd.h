@@ -143,7 +143,9 @@ int locomp_amd_dequant_int8(const void* W, const void* SCALES, void* OUT,
  * (row 2i + p = part p of row i) that take the bf16 kernels (2 M <= 64 the
  * decode kernels, else the MFMA GEMM, G % 32 == 0), whose stores add each
  * row's two part products (error at most 2^-16 sum_k |x_k w_nk| beyond
- * fp32 summation).  Scale groups G % 32 != 0 (G % 8 == 0; int8 G % 4),
+ * fp32 summation).  int4 scale groups G % 16 == 0 but G % 32 != 0 at
+ * M <= 2 (fp32: M = 1, K <= 4096) take the row kernel with a scale per 16 k;
+ * other scale groups G % 32 != 0 (G % 8 == 0; int8 G % 4),
  * operands aligned to 4 but not 16 bytes, fp32 shapes below 2^24
  * multiply-adds and a capture on a stream without the part-row workspace
  * take a VALU kernel with fp32 FMAs (fp16 / bf16: exact dot2 products);
