@@ -304,6 +304,42 @@ def test_int4_segment_decode_with_sixteenth():
         assert abs(got - want) < 1e-9
 
 
+def test_row_kernel_half_group_sums():
+    """gemv_rows_kernel with G16 (scale groups of 16-k multiples): a lane's 32 k
+    are 4 dwords of 8 k; dwords 0, 1 form the first 16 k and 2, 3 the second,
+    each half with its own scale and its own bias correction (1032 x the sum
+    of that half's activations).  Replayed on every dword pattern against the
+    plain dot product with a scale per 16 k, and the group of each half is
+    one group for every G % 16 == 0 (a lane's range starts at a multiple of 32)."""
+    rng = np.random.default_rng(2)
+    ws = _words()
+    for t in range(200):
+        x = rng.standard_normal(32).astype(np.float16)
+        s = rng.uniform(0.001, 0.01, 2)
+        wd = [ws[(4 * t + e) % len(ws)] for e in range(4)]
+        acc = 0.0
+        for h in range(2):
+            pe, xsum = 0.0, 0.0
+            for e in (2 * h, 2 * h + 1):
+                xe = x[8 * e: 8 * e + 8]
+                xd = xe.view(np.uint32)
+                xp = [_perm(xd[2], xd[0], 0x05040100), _perm(xd[2], xd[0], 0x07060302),
+                      _perm(xd[3], xd[1], 0x05040100), _perm(xd[3], xd[1], 0x07060302)]
+                xs = np.array(xp, np.uint32).view(np.float16).astype(np.float64)
+                r = [(wd[e] >> (4 * i)) & 0x000F000F | 0x64006400 for i in range(4)]
+                v = np.array(r, np.uint32).view(np.float16).astype(np.float64)
+                pe += float(np.dot(xs, v))
+                xsum += float(np.sum(xs))
+            acc += (pe - 1032.0 * xsum) * s[h]
+        q = np.array([n for w in wd for n in _nibbles(w)], np.float64) - 8
+        want = float(np.dot(x.astype(np.float64), q * np.repeat(s, 16)))
+        assert abs(acc - want) <= 1e-9 * max(1.0, abs(want))
+    for G in range(16, 1025, 16):
+        for k0 in range(0, 8 * G, 32):
+            for h in range(2):
+                assert (k0 + 16 * h) // G == (k0 + 16 * h + 15) // G
+
+
 def test_int8_decodes_exact():
     for w in _words():
         b = [((w >> (8 * i)) & 0xFF) for i in range(4)]
