@@ -142,13 +142,15 @@ static int launch_gemv_rows_m(const void* X, const void* W, const void* S, void*
       return launch_gemv_rows_t<M_, 3, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
     }
   }
-  if (nseg <= 4) return launch_gemv_rows_t<M_, 4, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
+  // (M = 2 takes K <= 4096, two segments: the longer forms are M = 1 only)
   if constexpr (M_ == 1) {
+    if (nseg <= 4) return launch_gemv_rows_t<M_, 4, 2, SD, OD, EPI>(X, W, S, O, M, N, K, G, st);
     // 6 segments: 181 VGPRs, sized for 2 workgroups per CU (3 measured slower)
     if (nseg <= 6) return launch_gemv_rows_t<M_, 6, 2, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
+    // 8 segments (K <= 16384): 237 VGPRs, sized for 2 workgroups per CU
+    return launch_gemv_rows_t<M_, 8, 2, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
   }
-  // 8 segments (K <= 16384, M = 1): 237 VGPRs, sized for 2 workgroups per CU
-  return launch_gemv_rows_t<M_, 8, 2, SD, OD, EPI, 2>(X, W, S, O, M, N, K, G, st);
+  return LQ_ERR_SHAPE;
 }
 
 template <int M_, int NSEG, int RW, int SD, int OD>
@@ -167,9 +169,15 @@ static int launch_gemv_diag_m(const void* X, const void* W, const void* S, void*
   const int64_t nseg = (K + 2047) / 2048;
   constexpr int rw2 = M_ <= 2 ? 4 : 2;
   if (nseg <= 1) return launch_gemv_diag_t<M_, 1, rw2 * 2, SD, OD>(X, W, S, O, M, N, K, G, st);
-  if (nseg <= 2) return launch_gemv_diag_t<M_, 2, rw2, SD, OD>(X, W, S, O, M, N, K, G, st);
-  if (nseg <= 4) return launch_gemv_diag_t<M_, 4, (rw2 > 1 ? rw2 / 2 : 1), SD, OD>(X, W, S, O, M, N, K, G, st);
-  return launch_gemv_diag_t<M_, 8, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+  // (the segment counts gemv_diag_ok admits: 2 up to M = 2, 8 at M = 1)
+  if constexpr (M_ <= 2) {
+    if (nseg <= 2) return launch_gemv_diag_t<M_, 2, rw2, SD, OD>(X, W, S, O, M, N, K, G, st);
+  }
+  if constexpr (M_ == 1) {
+    if (nseg <= 4) return launch_gemv_diag_t<M_, 4, (rw2 > 1 ? rw2 / 2 : 1), SD, OD>(X, W, S, O, M, N, K, G, st);
+    return launch_gemv_diag_t<M_, 8, 1, SD, OD>(X, W, S, O, M, N, K, G, st);
+  }
+  return LQ_ERR_SHAPE;
 }
 
 template <int M_, int NSEG, int RW, int SD, int OD>
