@@ -17,8 +17,8 @@ static int launch_rows16_t(const void* X, const void* W, const void* S, void* O,
 }
 
 // Segment counts and rows per wave as the G % 32 row kernel takes them, with
-// one row per wave from 5 segments (the second scale per lane k-range costs
-// registers).
+// one row per wave from 5 segments (the epilogue's gate / up pairs keep two)
+// since the second scale per lane k-range costs registers.
 template <int M_, int XD, bool EPI>
 static int launch_rows16_m(const void* X, const void* W, const void* S, void* O, int64_t M, int64_t N,
                            int64_t K, int64_t G, int sd, int od, hipStream_t st) {
