@@ -340,6 +340,62 @@ def test_row_kernel_half_group_sums():
                 assert (k0 + 16 * h) // G == (k0 + 16 * h + 15) // G
 
 
+def _rows16_plan(M, N, K, xd, epi):
+    """Segments and rows per wave launch_rows16_m picks (None: not launched)."""
+    nseg = (K + 2047) // 2048
+    if nseg <= 2 and N <= 3072:
+        return nseg, (2 if epi else 1)
+    if nseg <= 2:
+        return nseg, 4
+    if M == 1 and xd != "f32":
+        if nseg <= 4:
+            return 4, 2
+        if nseg <= 6:
+            return 6, (2 if epi else 1)
+        if not epi:
+            return 8, 1
+    return None
+
+
+@pytest.mark.parametrize("M,N,K,G,xd,sd,epi", [
+    (1, 11008, 4096, 16, "f16", "f16", False), (2, 1000, 4096, 16, "bf16", "f32", False),
+    (1, 700, 10240, 16, "f16", "bf16", False), (1, 513, 14400, 48, "bf16", "f32", False),
+    (2, 3000, 1440, 48, "f16", "f16", False), (1, 4100, 2080, 80, "f32", "f32", False),
+    (1, 3072, 576, 16, "f32", "f32", True), (2, 2000, 4096, 16, "f16", "f32", True),
+    (1, 1536, 12288, 48, "bf16", "bf16", True), (1, 1, 32, 16, "f16", "f32", False),
+    (1, 7, 16352, 16, "f16", "f32", False), (2, 4098, 4096, 16, "bf16", "f16", True),
+])
+def test_row_kernel_g16_addresses_in_bounds(M, N, K, G, xd, sd, epi):
+    """Every global load of gemv_rows_kernel in its G16 form, replayed for the
+    grid launch_rows16_m picks: activations (clamped row and k-range), weights
+    (clamped row), and each half's scale lie inside their arrays, and each
+    half's 16 k lie in the group whose scale it loads."""
+    plan = _rows16_plan(M, N, K, xd, epi)
+    assert plan is not None
+    nseg, rw = plan
+    m_ = 1 if M == 1 else 2
+    blocks = (N + 4 * rw - 1) // (4 * rw)
+    ns = K // G
+    xs, ss = (4 if xd == "f32" else 2), (4 if sd == "f32" else 2)
+    n0 = (np.arange(blocks * 4, dtype=np.int64) * rw)[:, None, None]
+    c = np.arange(nseg, dtype=np.int64)[None, :, None]
+    lane = np.arange(64, dtype=np.int64)[None, None, :]
+    k0 = np.minimum(c * 2048 + lane * 32, K - 32)
+    assert k0.min() >= 0
+    for m in range(m_):
+        me = m if m < M else 0
+        at = me * K + k0 + 8 * np.arange(4)[:, None, None, None]
+        assert at.min() >= 0 and (at.max() + 8) * xs <= M * K * xs
+    for r in range(rw):
+        n = np.minimum(n0 + r, N - 1)
+        assert ((n * (K // 2) + k0 // 2).max() + 16) <= N * K // 2
+        for h in range(2):
+            kh = k0 + 16 * h
+            si = n * ns + kh // G
+            assert si.min() >= 0 and (si.max() + 1) * ss <= N * ns * ss
+            assert np.array_equal(kh // G, (kh + 15) // G)
+
+
 def test_int8_decodes_exact():
     for w in _words():
         b = [((w >> (8 * i)) & 0xFF) for i in range(4)]
